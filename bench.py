@@ -1,0 +1,384 @@
+"""Benchmark of the decode-step hot path on one MI355X.
+
+Headline (the JSON `value`): fp16 split-K GQA decode attention at the
+Llama-3-8B decode shape B=8, H=32, Hkv=8, D=128, S=4096 — one step is one
+decode_attention call over one batch of synthetic inputs. The other
+BASELINE.json configs (INT8 / INT4 KIVI attention, the KV writers, W4A16 at
+M in {1, 16, 128} on the three Llama shapes, the S / B sweep) are measured
+the same way and reported under "details".
+
+Method
+  * Inputs are generated on the GPU from a seeded generator and are resident
+    in HBM before timing. Each config rotates over enough distinct input
+    sets (>= 768 MB in total) that every step reads from HBM rather than the
+    256 MB Infinity Cache.
+  * The K timed steps are captured in one HIP graph on a dedicated stream and
+    replayed once; HIP events recorded on that stream bracket the replay,
+    with torch.cuda.synchronize() on both sides. Per-launch time = elapsed/K.
+  * Before timing, every config is checked against an fp32 torch computation
+    on the GPU (max-abs 2e-3); a failing config aborts the run.
+  * roofline.achieved = algorithmic bytes per launch / per-launch time, with
+    the byte counts stated in DESIGN.md; peak = 8 TB/s (MI355X HBM3E).
+  * cpu_baseline: the oracle's eager fp32 attention (the reference's
+    repeat_interleave form, oracle/attention.py) on the host cores, timed on
+    a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-details] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "llm-inference-kernels_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 768 << 20
+GATE_TOL = 2e-3
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------- byte accounting
+
+def attn_bytes(fmt: str, B: int, H: int, Hkv: int, S: int, D: int = 128, gs: int = 128) -> int:
+    qo = 2 * B * H * D * 2
+    if fmt == "fp16":
+        return 2 * B * Hkv * S * D * 2 + qo
+    if fmt == "int8":
+        return 2 * (B * Hkv * S * D + 2 * B * Hkv * S) + qo
+    if fmt == "int4":
+        return B * Hkv * S * D + 2 * B * Hkv * ((S + gs - 1) // gs) * D + 2 * B * Hkv * S + qo
+    raise ValueError(fmt)
+
+
+def w4a16_bytes(M: int, K: int, N: int, gs: int = 128) -> int:
+    return K * N // 2 + 2 * (K // gs) * N + 2 * M * K + 2 * M * N
+
+
+# ----------------------------------------------------------------- timing
+
+def time_steps(steps_fns, warmup: int, reps: int):
+    """Warm up eagerly, capture `reps` steps (cycling through steps_fns) in a
+    HIP graph and time one replay with events on the capture stream.
+    Returns per-step microseconds."""
+    import torch
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(max(warmup, len(steps_fns))):
+            steps_fns[i % len(steps_fns)]()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(reps):
+            steps_fns[i % len(steps_fns)]()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    graph.replay()           # one untimed replay (page-in of the graph itself)
+    torch.cuda.synchronize()
+    start.record(stream)
+    graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / reps
+    del graph
+    return us
+
+
+def n_sets_for(bytes_per_set: int) -> int:
+    return max(2, min(16, math.ceil(ROTATE_BYTES / max(1, bytes_per_set))))
+
+
+# ------------------------------------------------------------ correctness gates
+
+def torch_attention_ref(q, k, v, scale):
+    """fp32 GQA attention on the GPU (grouped, no KV expansion)."""
+    import torch
+    B, H, D = q.shape
+    Hkv = k.shape[1]
+    G = H // Hkv
+    qf = q.float().reshape(B, Hkv, G, D)
+    s = torch.matmul(qf, k.float().transpose(-1, -2).contiguous()) * scale
+    p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, v.float()).reshape(B, H, D)
+
+
+def gate(name: str, got, ref) -> float:
+    err = float((got.float() - ref.float()).abs().max())
+    if not err <= GATE_TOL:
+        raise SystemExit(f"correctness gate failed for {name}: max-abs {err:.3e} > {GATE_TOL}")
+    return err
+
+
+# ------------------------------------------------------------------ configs
+
+def bench_attention(llmik, fmt: str, B: int, S: int, steps: int, warmup: int, gs: int = 128,
+                    H: int = 32, Hkv: int = 8, seed: int = 0):
+    import torch
+    dev = torch.device("cuda:0")
+    D = 128
+    scale = 1.0 / math.sqrt(D)
+    nbytes = attn_bytes(fmt, B, H, Hkv, S, D, gs)
+    n_sets = n_sets_for(nbytes)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    sets = []
+    for _ in range(n_sets):
+        q = torch.randn((B, H, D), generator=gen, device=dev, dtype=torch.float16)
+        k = torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16)
+        v = torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16)
+        if fmt != "fp16":
+            k[..., [3, 37, 71, 105]] *= 10
+        if fmt == "fp16":
+            sets.append((q, k, v))
+        elif fmt == "int8":
+            sets.append((q, *llmik.quantize_per_token(k), *llmik.quantize_per_token(v)))
+        else:
+            sets.append((q, *llmik.quantize_k_per_channel_groupwise_int4(k, gs),
+                         *llmik.quantize_v_per_token_int4(v)))
+        del k, v
+    # correctness gate on the first set (first <= 8 sequences)
+    gb = min(B, 8)
+    if fmt == "fp16":
+        q0, k0, v0 = sets[0]
+        got = llmik.decode_attention(q0, k0, v0, scale)
+        kd, vd = k0[:gb], v0[:gb]
+    elif fmt == "int8":
+        q0, kq, ks, vq, vs = sets[0]
+        got = llmik.decode_attention_int8(q0, kq, ks, vq, vs, scale)
+        kd = kq[:gb].float() * ks[:gb].float()[..., None]
+        vd = vq[:gb].float() * vs[:gb].float()[..., None]
+    else:
+        q0, kq, ks, vq, vs = sets[0]
+        got = llmik.decode_attention_int4(q0, kq, ks, vq, vs, gs, scale)
+        kd = unpack_int4(kq[:gb]).float() * ks[:gb].float().repeat_interleave(gs, dim=2)[:, :, :S]
+        vd = unpack_int4(vq[:gb]).float() * vs[:gb].float()[..., None]
+    err = gate(f"{fmt} attention B={B} S={S}", got[:gb],
+               torch_attention_ref(q0[:gb], kd, vd, scale))
+    del kd, vd, got
+
+    if fmt == "fp16":
+        fns = [lambda s=s: llmik.decode_attention(s[0], s[1], s[2], scale) for s in sets]
+    elif fmt == "int8":
+        fns = [lambda s=s: llmik.decode_attention_int8(s[0], s[1], s[2], s[3], s[4], scale)
+               for s in sets]
+    else:
+        fns = [lambda s=s: llmik.decode_attention_int4(s[0], s[1], s[2], s[3], s[4], gs, scale)
+               for s in sets]
+    us = time_steps(fns, warmup, steps)
+    del sets, fns
+    torch.cuda.empty_cache()
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"name": f"attn_{fmt}" + (f"_g{gs}" if fmt == "int4" else ""), "B": B, "S": S,
+            "us": round(us, 3), "bytes": nbytes, "GBps": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "max_abs_err": err, "sets": n_sets}
+
+
+def unpack_int4(p):
+    import torch
+    x = p.to(torch.int32) & 0xFF
+    lo = ((x & 0x0F) << 28) >> 28
+    hi = ((x & 0xF0) << 24) >> 28
+    return torch.stack([lo, hi], dim=-1).reshape(*p.shape[:-1], 2 * p.shape[-1])
+
+
+def bench_w4a16(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int = 128,
+                seed: int = 0):
+    import torch
+    dev = torch.device("cuda:0")
+    nbytes = w4a16_bytes(M, K, N, gs)
+    n_sets = n_sets_for(nbytes)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    sets = []
+    for _ in range(n_sets):
+        # random packed words: every nibble pattern, codes in [-8, 7]
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), generator=gen, device=dev,
+                          dtype=torch.int32)
+        sc = (torch.rand((K // gs, N), generator=gen, device=dev) * 0.004 + 0.001).half()
+        a = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float16)
+        sets.append((a, w, sc))
+    a0, w0, s0 = sets[0]
+    got = llmik.w4a16_gemm_f32out(a0, w0, s0, gs)
+    ref = a0.float() @ unpack_w4(w0).float().mul(s0.float().repeat_interleave(gs, dim=0))
+    err = gate(f"w4a16 M={M} K={K} N={N}", got, ref)
+    del ref, got
+    fns = [lambda s=s: llmik.w4a16_gemm(s[0], s[1], s[2], gs) for s in sets]
+    us = time_steps(fns, warmup, steps)
+    del sets, fns
+    torch.cuda.empty_cache()
+    gbs = nbytes / (us * 1e-6) / 1e9
+    flops = 2.0 * M * K * N
+    tf = flops / (us * 1e-6) / 1e12
+    return {"name": "w4a16", "M": M, "K": K, "N": N, "us": round(us, 3), "bytes": nbytes,
+            "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "TFLOPs": round(tf, 2), "frac_mfma_fp16_peak": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
+            "max_abs_err_f32out": err, "sets": n_sets}
+
+
+def unpack_w4(w):
+    import torch
+    shifts = torch.arange(8, device=w.device, dtype=torch.int32).view(1, 8, 1) * 4
+    x = (w.unsqueeze(1) << (28 - shifts)) >> 28
+    return x.reshape(w.shape[0] * 8, w.shape[1])
+
+
+def bench_writers(llmik, B: int, S: int, steps: int, warmup: int, seed: int = 0):
+    import torch
+    dev = torch.device("cuda:0")
+    out = []
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    x_bytes = B * 8 * S * 128 * 2
+    n_sets = n_sets_for(x_bytes)
+    xs = [torch.randn((B, 8, S, 128), generator=gen, device=dev, dtype=torch.float16)
+          for _ in range(n_sets)]
+    cases = [
+        ("quantize_per_token_int8", lambda x: llmik.quantize_per_token(x),
+         x_bytes + B * 8 * S * 128 + B * 8 * S * 2),
+        ("quantize_k_groupwise_int4_g128", lambda x: llmik.quantize_k_per_channel_groupwise_int4(x, 128),
+         x_bytes + B * 8 * S * 64 + B * 8 * ((S + 127) // 128) * 128 * 2),
+        ("quantize_v_per_token_int4", lambda x: llmik.quantize_v_per_token_int4(x),
+         x_bytes + B * 8 * S * 64 + B * 8 * S * 2),
+    ]
+    for name, fn, nbytes in cases:
+        fns = [lambda x=x, fn=fn: fn(x) for x in xs]
+        us = time_steps(fns, warmup, steps)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append({"name": name, "B": B, "S": S, "us": round(us, 3), "bytes": nbytes,
+                    "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+    del xs
+    torch.cuda.empty_cache()
+    return out
+
+
+# -------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(budget_s: float = 15.0):
+    """Time the oracle's eager fp32 attention (reference form) on the host."""
+    import numpy as np
+    from oracle import attention as oa
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()
+                       if i.get("user_api") == "blas"), default=1)
+    except Exception:   # pragma: no cover
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    B, H, Hkv, S, D = 8, 32, 8, 4096, 128
+    q = rng.standard_normal((B, H, D)).astype(np.float16)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+    oa.decode_attention_expanded(q, k, v)        # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter_ns()
+        oa.decode_attention_expanded(q, k, v)
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+        if len(times) >= 50:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(med, 1), "unit": "us", "cores": int(threads), "kind": "port",
+            "sample": f"{len(times)} full calls of oracle/attention.py decode_attention_expanded "
+                      f"(eager fp32, repeat_interleave GQA) at B=8 H=32 Hkv=8 D=128 S=4096, "
+                      f"median; numpy BLAS threads={threads}"}
+
+
+# ---------------------------------------------------------------------- main
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-details", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list: attn,int8,int4,w4a16,writers,sweep")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are out of scope "
+                                   "(bench.py --gpus must be 1)"}))
+        sys.exit(2)
+
+    import torch
+    import llmik_cuda as llmik
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    log(f"device {torch.cuda.get_device_name(0)}; library {llmik.LIB_PATH}")
+
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda k: not only or k in only)
+
+    t_wall = time.perf_counter()
+    head = bench_attention(llmik, "fp16", 8, 4096, args.steps, args.warmup, seed=1)
+    log(f"headline {head}")
+    details = []
+    if not args.no_details:
+        if want("int8"):
+            details.append(bench_attention(llmik, "int8", 8, 4096, 100, 10, seed=2))
+            log(details[-1])
+        if want("int4"):
+            for B, S in ((8, 4096), (64, 8192)):
+                details.append(bench_attention(llmik, "int4", B, S, 100 if B == 8 else 30, 10,
+                                               gs=128, seed=3))
+                log(details[-1])
+            details.append(bench_attention(llmik, "fp16", 64, 8192, 20, 5, seed=4))
+            log(details[-1])
+        if want("sweep"):
+            for B, S in ((8, 1024), (8, 16384), (8, 32768), (1, 4096), (64, 4096)):
+                details.append(bench_attention(llmik, "fp16", B, S, 50, 5, seed=5))
+                log(details[-1])
+        if want("w4a16"):
+            for M in (1, 16, 128):
+                for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
+                    details.append(bench_w4a16(llmik, M, K, N, 100 if M < 128 else 30, 10, seed=6))
+                    log(details[-1])
+        if want("writers"):
+            details.extend(bench_writers(llmik, 8, 4096, 50, 5, seed=7))
+            log(details[-3:])
+    gpu_wall = time.perf_counter() - t_wall
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline()
+        log(f"cpu baseline {cpu}")
+
+    achieved = head["GBps"]
+    line = {
+        "metric": "decode-attn µs + % HBM peak; W4A16 GEMV µs at Llama-3-8B shapes",
+        "value": head["us"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "fp16 split-K GQA decode attention (Llama-3-8B heads)",
+                   "batch": 8, "n_heads": 32, "n_kv_heads": 8, "head_dim": 128,
+                   "seqlen_kv": 4096, "kv_layout": "[B, Hkv, S, D] fp16 contiguous",
+                   "input_sets_rotated": head["sets"]},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": head["bytes"]},
+        "cpu_baseline": cpu,
+        "details": details,
+        "gpu_wall_s": round(gpu_wall, 1),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

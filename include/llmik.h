@@ -1,0 +1,227 @@
+/*
+ * llmik.h — C ABI of the gfx950 decode-step hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), enqueues its kernels asynchronously on that stream and
+ * returns an llmik_status. Nothing here allocates device memory: outputs
+ * and the optional workspace are supplied by the caller. No torch types
+ * appear in any signature.
+ *
+ * Each function cites the reference operator it replaces: the torch op in
+ * bindings/extension.cpp of bundle-adjuster/llm-inference-kernels and the
+ * CUDA launcher behind it.
+ *
+ * Tensor conventions (row-major, contiguous, 16-byte aligned base pointers):
+ *   fp16 tensors are IEEE binary16 bit patterns (uint16_t);
+ *   int8 codes are int8_t; packed int4 is one byte per two codes with the
+ *   even channel in the low nibble; W4 weights are uint32 words holding
+ *   8 codes along K (bits 4i..4i+3 = K position 8*k_pack + i).
+ *
+ * Workspace contract (attention and W4A16): query the size with the
+ * matching *_workspace_size function. The start of the workspace holds
+ * completion counters that must be zero before the first use; every
+ * successful call leaves them zero again, so one zero-filled buffer can be
+ * reused by consecutive calls on one stream. Calls that share a workspace
+ * must not run concurrently.
+ */
+#ifndef LLMIK_H
+#define LLMIK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLMIK_API __attribute__((visibility("default")))
+
+typedef int llmik_status;
+#define LLMIK_OK 0
+/* Negative codes are argument/usage errors detected before any launch;
+ * positive codes are hipError_t values returned by the HIP runtime. */
+#define LLMIK_ERR_INVALID (-1)
+#define LLMIK_ERR_UNSUPPORTED (-2)
+#define LLMIK_ERR_WORKSPACE (-3)
+#define LLMIK_ERR_ALIGNMENT (-4)
+
+/* Message for the last error raised on the calling thread ("" if none). */
+LLMIK_API const char* llmik_last_error(void);
+/* ABI version; bumped on any signature change. */
+LLMIK_API int llmik_abi_version(void);
+
+/* ---------------------------------------------------------------- attention
+ * Workspace bytes needed by the decode-attention entry points for this
+ * shape on the current device (0 means none needed; pass NULL).
+ */
+LLMIK_API size_t llmik_attention_workspace_size(int batch, int n_heads, int n_kv_heads,
+                                                int seqlen, int head_dim);
+
+/*
+ * fp16-KV split-K GQA decode attention.
+ * Replaces: decode_attention op (bindings/extension.cpp:26-83) and
+ *   launch_decode_attention_splitk / decode_attention_n_splits
+ *   (kernels/attention/fused_attention.cuh:32-41,
+ *   kernels/attention/fused_attention_splitk.cu:64-66,233-250); also serves
+ *   decode_attention_v3 (bindings/extension.cpp:89-115; launch_decode_attention,
+ *   kernels/attention/fused_attention.cuh:17-20, fused_attention.cu:110-119)
+ *   with seqlen == kv_buf_len, since the result semantics are identical.
+ *   q   [batch, n_heads, head_dim] fp16
+ *   k,v [batch, n_kv_heads, kv_buf_len, head_dim] fp16; positions
+ *       [0, seqlen) are read (seqlen <= kv_buf_len)
+ *   out [batch, n_heads, head_dim] fp16
+ * head_dim must be 128; n_heads must be a multiple of n_kv_heads.
+ */
+LLMIK_API llmik_status llmik_decode_attention_f16(
+    const void* q, const void* k, const void* v, void* out,
+    int batch, int n_heads, int n_kv_heads, int seqlen, int head_dim, int kv_buf_len,
+    float softmax_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * INT8 per-token KV decode attention with fused dequantisation.
+ * Replaces: decode_attention_int8 op (bindings/extension.cpp:152-194) and
+ *   launch_decode_attention_int8 (kernels/attention/fused_attention.cuh:54-60,
+ *   kernels/attention/fused_attention_int8.cu:109-122).
+ *   k_q,v_q         [batch, n_kv_heads, kv_buf_len, head_dim] int8
+ *   k_scale,v_scale [batch, n_kv_heads, kv_buf_len] fp16
+ * The reference op has no live-length argument; seqlen == kv_buf_len
+ * reproduces it. seqlen < kv_buf_len reads a preallocated cache in place.
+ */
+LLMIK_API llmik_status llmik_decode_attention_int8(
+    const void* q, const void* k_q, const void* k_scale, const void* v_q, const void* v_scale,
+    void* out, int batch, int n_heads, int n_kv_heads, int seqlen, int head_dim, int kv_buf_len,
+    float softmax_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * INT4 KIVI KV decode attention (K per-channel groupwise, V per-token,
+ * symmetric, packed) with fused dequantisation.
+ * Replaces: decode_attention_int4 op (bindings/extension.cpp:269-314) and
+ *   launch_decode_attention_int4 (kernels/attention/fused_attention.cuh:73-80,
+ *   kernels/attention/fused_attention_int4.cu:120-135).
+ *   k_q,v_q [batch, n_kv_heads, kv_buf_len, head_dim/2] int8 (packed int4)
+ *   k_scale [batch, n_kv_heads, n_groups, head_dim] fp16; token t uses
+ *           group t / group_size (needs n_groups >= ceil(seqlen/group_size))
+ *   v_scale [batch, n_kv_heads, kv_buf_len] fp16
+ */
+LLMIK_API llmik_status llmik_decode_attention_int4(
+    const void* q, const void* k_q, const void* k_scale, const void* v_q, const void* v_scale,
+    void* out, int batch, int n_heads, int n_kv_heads, int seqlen, int head_dim, int kv_buf_len,
+    int group_size, int n_groups, float softmax_scale, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* --------------------------------------------------------------- KV writers
+ * Bit-exact symmetric quantisers: scale = max(absmax/qmax, 1e-8) in fp32
+ * with IEEE division, q = clamp(round_half_even(x / scale), -qmax, qmax),
+ * scale stored as fp16 (round to nearest even). This is
+ * reference/kv_cache_ref.py applied to x.float().
+ */
+
+/*
+ * INT8 per-token quantisation (qmax 127).
+ * Replaces: quantize_per_token op (bindings/extension.cpp:120-146) and
+ *   launch_quantize_per_token (kernels/kv_cache/kv_compress.cuh:19-22,
+ *   kernels/kv_cache/kv_compress.cu:69-79).
+ *   x [batch, n_kv_heads, seqlen, head_dim] fp16 -> q int8 same shape,
+ *   scale [batch, n_kv_heads, seqlen] fp16.
+ */
+LLMIK_API llmik_status llmik_quantize_per_token_int8(
+    const void* x, void* q, void* scale, int batch, int n_kv_heads, int seqlen, int head_dim,
+    void* stream);
+
+/*
+ * INT4 K quantisation, per channel, grouped along the sequence (qmax 7).
+ * Replaces: quantize_k_per_channel_groupwise_int4 op
+ *   (bindings/extension.cpp:200-229) and its launcher
+ *   (kernels/kv_cache/kv_compress.cuh:35-39, kv_compress.cu:159-170).
+ *   x [batch, n_kv_heads, seqlen, head_dim] fp16 ->
+ *   q [batch, n_kv_heads, seqlen, head_dim/2] packed int4,
+ *   scale [batch, n_kv_heads, ceil(seqlen/group_size), head_dim] fp16.
+ *   A short final group uses only its real tokens.
+ */
+LLMIK_API llmik_status llmik_quantize_k_per_channel_groupwise_int4(
+    const void* x, void* q, void* scale, int batch, int n_kv_heads, int seqlen, int head_dim,
+    int group_size, void* stream);
+
+/*
+ * INT4 V quantisation, per token (qmax 7).
+ * Replaces: quantize_v_per_token_int4 op (bindings/extension.cpp:235-261)
+ *   and its launcher (kernels/kv_cache/kv_compress.cuh:45-48,
+ *   kv_compress.cu:219-228).
+ *   x [batch, n_kv_heads, seqlen, head_dim] fp16 ->
+ *   q [batch, n_kv_heads, seqlen, head_dim/2] packed int4,
+ *   scale [batch, n_kv_heads, seqlen] fp16.
+ */
+LLMIK_API llmik_status llmik_quantize_v_per_token_int4(
+    const void* x, void* q, void* scale, int batch, int n_kv_heads, int seqlen, int head_dim,
+    void* stream);
+
+/* -------------------------------------------------------------------- W4A16
+ * out[M, N] = act[M, K] @ dequant(W)[K, N], W[k, n] = q[k, n] * scale[k/g, n],
+ * fp32 accumulation.
+ *   act           [M, K] fp16
+ *   weight_packed [K/8, N] uint32 (int4 along K)
+ *   scale         [K/group_size, N] fp16
+ * group_size must be a positive multiple of 8 dividing K.
+ */
+LLMIK_API size_t llmik_w4a16_workspace_size(int M, int N, int K, int group_size);
+
+/*
+ * Replaces: w4a16_gemm op (bindings/extension.cpp:322-376) and
+ *   launch_w4a16_gemm / launch_w4a16_gemm_splitk / w4a16_n_splits
+ *   (kernels/quant/quant_matmul.cuh:30-44, quant_matmul.cu:642-652,778-856).
+ *   out [M, N] fp16.
+ */
+LLMIK_API llmik_status llmik_w4a16_gemm(
+    const void* act, const void* weight_packed, const void* scale, void* out,
+    int M, int N, int K, int group_size, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Same kernels with an fp32 output (the accumulator before fp16 rounding).
+ * No reference counterpart: it exists so the 2e-3 max-abs gate against an
+ * fp32-accumulated oracle can be checked without fp16 output rounding.
+ */
+LLMIK_API llmik_status llmik_w4a16_gemm_f32out(
+    const void* act, const void* weight_packed, const void* scale, void* out_f32,
+    int M, int N, int K, int group_size, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Materialise fp16 W[k, n] = fp16(q[k, n] * scale[k/g, n]).
+ * Replaces: w4a16_dequantize op (bindings/extension.cpp:382-403) and
+ *   launch_w4a16_dequantize (kernels/quant/quant_matmul.cuh:58-60;
+ *   kernels/quant/quant_matmul.cu:629-638). out [K, N] fp16.
+ */
+LLMIK_API llmik_status llmik_w4a16_dequantize(
+    const void* weight_packed, const void* scale, void* out, int K, int N, int group_size,
+    void* stream);
+
+/* ------------------------------------------------------ fused elementwise ops */
+
+/*
+ * out[r, :] = fp16(x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * weight), fp32 math.
+ * Replaces: rmsnorm op (bindings/extension.cpp:408-424) and launch_rmsnorm
+ *   (kernels/fused/fused_ops.cuh:9-11, kernels/fused/fused_ops.cu:96-100).
+ */
+LLMIK_API llmik_status llmik_rmsnorm(const void* x, const void* weight, void* out, int rows,
+                                     int hidden, float eps, void* stream);
+
+/*
+ * out = fp16(silu(gate) * up), elementwise over n values.
+ * Replaces: silu_mul op (bindings/extension.cpp:427-441) and launch_silu_mul
+ *   (kernels/fused/fused_ops.cuh:13-14, kernels/fused/fused_ops.cu:102-107).
+ */
+LLMIK_API llmik_status llmik_silu_mul(const void* gate, const void* up, void* out, long n,
+                                      void* stream);
+
+/*
+ * out = x * cos + rotate_half(x) * sin, x [B, H, S, D], cos/sin [B, S, D].
+ * Replaces: rope op (bindings/extension.cpp:446-473) and launch_rope
+ *   (kernels/fused/fused_ops.cuh:17-18, kernels/fused/fused_ops.cu:88-94).
+ */
+LLMIK_API llmik_status llmik_rope(const void* x, const void* cos, const void* sin, void* out,
+                                  int B, int H, int S, int D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMIK_H */

@@ -1,0 +1,122 @@
+// Device-side helpers shared by every gfx950 kernel in this library.
+//
+// Everything here is written for CDNA4 wave64: cross-lane traffic uses DPP
+// row operations (a DPP "row" is 16 lanes), vector memory uses 16-byte
+// global loads, and fp16 <-> fp32 conversion goes through the hardware
+// converters (round-to-nearest-even).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace llmik {
+
+constexpr int kWave = 64;
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- DPP row (16-lane) reductions -----------------------------------------
+// DPP control codes (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), Ctrl, 0xF, 0xF, true));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the result.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<kDppQuadXor1>(v);
+    v += dpp_f32<kDppQuadXor2>(v);
+    v += dpp_f32<kDppRowHalfMirror>(v);
+    v += dpp_f32<kDppRowMirror>(v);
+    return v;
+}
+
+// Max over the 16 lanes of a DPP row; every lane of the row gets the result.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppRowMirror>(v));
+    return v;
+}
+
+// ---- conversions ----------------------------------------------------------
+__device__ __forceinline__ float h2f(uint16_t bits) {
+    return (float)__builtin_bit_cast(f16, bits);
+}
+
+__device__ __forceinline__ uint16_t f2h_bits(float x) {
+    return __builtin_bit_cast(uint16_t, (f16)x);  // v_cvt_f16_f32, RNE
+}
+
+// Unpack 8 fp16 stored in a 16-byte vector into fp32.
+__device__ __forceinline__ void f16x8_to_f32(const u32x4 raw, float out[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const f16x2 h = __builtin_bit_cast(f16x2, raw[i]);
+        out[2 * i] = (float)h[0];
+        out[2 * i + 1] = (float)h[1];
+    }
+}
+
+// 8 signed int8 codes (two dwords, little-endian) -> fp32.
+__device__ __forceinline__ void i8x8_to_f32(const u32x2 raw, float out[8]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int32_t w = (int32_t)raw[i];
+        out[4 * i + 0] = (float)((w << 24) >> 24);
+        out[4 * i + 1] = (float)((w << 16) >> 24);
+        out[4 * i + 2] = (float)((w << 8) >> 24);
+        out[4 * i + 3] = (float)(w >> 24);
+    }
+}
+
+// 8 signed 4-bit codes in one dword -> fp32. Nibble i (bits 4i..4i+3) is
+// element i, two's complement. This is both the KV-cache byte packing
+// (even channel in the low nibble) and the W4 packing along K.
+__device__ __forceinline__ void i4x8_to_f32(const uint32_t raw, float out[8]) {
+    const int32_t w = (int32_t)raw;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = (float)((w << (28 - 4 * i)) >> 28);
+}
+
+// ---- buffer loads ---------------------------------------------------------
+__device__ __forceinline__ u32x4 load16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x2 load8(const void* p) {
+    return *reinterpret_cast<const u32x2*>(p);
+}
+__device__ __forceinline__ uint32_t load4(const void* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// ---- exact symmetric quantisation step ------------------------------------
+// Returns rint(x / s) with x / s the IEEE correctly rounded fp32 quotient,
+// which is what torch's CPU `x / scale` followed by `.round()` computes.
+// `r` must be the fp32 reciprocal of s. The product x*r is within ~2 ulp of
+// x/s, so it only decides the rounding when it is clear of a half-integer;
+// near a half-integer (where a 2-ulp error could flip the result, or where
+// the exact quotient is a tie that rounds to even) the true division runs.
+__device__ __forceinline__ float quant_round(float x, float s, float r) {
+    const float y = x * r;
+    const float k = __builtin_rintf(y);
+    const float frac = fabsf(y - k);
+    if (fabsf(frac - 0.5f) <= 1.0e-4f * fmaxf(1.0f, fabsf(y))) {
+        return __builtin_rintf(x / s);
+    }
+    return k;
+}
+
+}  // namespace llmik

@@ -1,0 +1,133 @@
+// Fused elementwise decode-path ops for gfx950: RMSNorm, SwiGLU, RoPE.
+// Semantics follow kernels/fused/fused_ops.cu:31-86 of the reference
+// (fp32 math, one fp16 rounding of each output).
+#include "device_common.hpp"
+#include "llmik_internal.hpp"
+
+namespace llmik {
+
+// One workgroup per row; 16-byte vectors when the row allows it.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ w,
+                                                      uint16_t* __restrict__ out, int hidden,
+                                                      float eps) {
+    const long row = blockIdx.x;
+    const uint16_t* xr = x + row * hidden;
+    uint16_t* orow = out + row * hidden;
+    const bool vec = (hidden % 8) == 0;
+    float ss = 0.0f;
+    if (vec) {
+        for (int i = threadIdx.x * 8; i < hidden; i += 256 * 8) {
+            float v[8];
+            f16x8_to_f32(load16(xr + i), v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+        }
+    } else {
+        for (int i = threadIdx.x; i < hidden; i += 256) {
+            const float v = h2f(xr[i]);
+            ss = fmaf(v, v, ss);
+        }
+    }
+    // wave sum: 16-lane rows, then across the 4 rows via LDS
+    ss = row16_sum(ss);
+    __shared__ float s_red[16];
+    if ((threadIdx.x & 15) == 0) s_red[threadIdx.x >> 4] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tot += s_red[r];
+    const float inv = 1.0f / sqrtf(tot / (float)hidden + eps);
+    if (vec) {
+        for (int i = threadIdx.x * 8; i < hidden; i += 256 * 8) {
+            float v[8], g[8];
+            f16x8_to_f32(load16(xr + i), v);
+            f16x8_to_f32(load16(w + i), g);
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = (uint32_t)f2h_bits(v[2 * e] * inv * g[2 * e]) |
+                       ((uint32_t)f2h_bits(v[2 * e + 1] * inv * g[2 * e + 1]) << 16);
+            *reinterpret_cast<u32x4*>(orow + i) = o;
+        }
+    } else {
+        for (int i = threadIdx.x; i < hidden; i += 256)
+            orow[i] = f2h_bits(h2f(xr[i]) * inv * h2f(w[i]));
+    }
+}
+
+__device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ g,
+                                                       const uint16_t* __restrict__ u,
+                                                       uint16_t* __restrict__ out, long n) {
+    const long i8 = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i8 + 8 <= n) {
+        float gv[8], uv[8];
+        f16x8_to_f32(load16(g + i8), gv);
+        f16x8_to_f32(load16(u + i8), uv);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = (uint32_t)f2h_bits(silu_mul1(gv[2 * e], uv[2 * e])) |
+                   ((uint32_t)f2h_bits(silu_mul1(gv[2 * e + 1], uv[2 * e + 1])) << 16);
+        *reinterpret_cast<u32x4*>(out + i8) = o;
+    } else {
+        for (long i = i8; i < n; ++i) out[i] = f2h_bits(silu_mul1(h2f(g[i]), h2f(u[i])));
+    }
+}
+
+// One thread per (b, h, s, d) with d < D/2: it produces out[d] and
+// out[d + D/2] from the pair (x[d], x[d + D/2]).
+__global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ x,
+                                                   const uint16_t* __restrict__ cs,
+                                                   const uint16_t* __restrict__ sn,
+                                                   uint16_t* __restrict__ out, int B, int H,
+                                                   int S, int D) {
+    const int half_d = D / 2;
+    const long total = (long)B * H * S * half_d;
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int d = (int)(idx % half_d);
+    const long bhs = idx / half_d;
+    const int s = (int)(bhs % S);
+    const int b = (int)(bhs / ((long)S * H));
+    const long xrow = bhs * D;
+    const long crow = ((long)b * S + s) * D;
+    const float x1 = h2f(x[xrow + d]);
+    const float x2 = h2f(x[xrow + d + half_d]);
+    // rotate_half(x) = [-x[D/2:], x[:D/2]]
+    out[xrow + d] = f2h_bits(x1 * h2f(cs[crow + d]) - x2 * h2f(sn[crow + d]));
+    out[xrow + d + half_d] = f2h_bits(x2 * h2f(cs[crow + d + half_d]) + x1 * h2f(sn[crow + d + half_d]));
+}
+
+int launch_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps,
+                   hipStream_t stream) {
+    if (rows == 0 || hidden == 0) return LLMIK_OK;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                       static_cast<uint16_t*>(out), hidden, eps);
+    return check_launch();
+}
+
+int launch_silu_mul(const void* g, const void* u, void* out, long n, hipStream_t stream) {
+    if (n == 0) return LLMIK_OK;
+    const long blocks = (n + 256 * 8 - 1) / (256 * 8);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
+                       static_cast<uint16_t*>(out), n);
+    return check_launch();
+}
+
+int launch_rope(const void* x, const void* cs, const void* sn, void* out, int B, int H, int S,
+                int D, hipStream_t stream) {
+    const long total = (long)B * H * S * (D / 2);
+    if (total == 0) return LLMIK_OK;
+    const long blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(cs),
+                       static_cast<const uint16_t*>(sn), static_cast<uint16_t*>(out), B, H, S, D);
+    return check_launch();
+}
+
+}  // namespace llmik

@@ -1,0 +1,89 @@
+// Host-side declarations shared by the kernel translation units and the
+// C ABI layer (capi.cpp). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/llmik.h"
+
+namespace llmik {
+
+constexpr int kMaxAttnSplits = 256;
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Records `msg` as the calling thread's last error and returns `code`.
+int set_error(int code, const char* msg);
+// Converts hipGetLastError() after a launch into an llmik_status.
+int check_launch();
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
+// ---- attention -------------------------------------------------------------
+struct AttnPlan {
+    int hpw;             // query heads per workgroup
+    int n_hchunks;       // head chunks per kv head
+    int n_splits;        // KV splits per (batch, kv head, head chunk)
+    int chunk;           // tokens per split (multiple of the 64-token step)
+    long n_slot_groups;  // batch * n_kv_heads * n_hchunks
+    size_t workspace_bytes;
+    size_t off_ml, off_o;
+};
+
+AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen);
+
+struct AttnLaunch {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* k_scale;
+    const void* v_scale;
+    void* out;
+    int batch, n_heads, n_kv_heads, seqlen, kv_buf_len;
+    int group_size, n_groups;
+    float softmax_scale;
+    void* workspace;
+    size_t workspace_bytes;
+};
+
+int launch_attention_f16(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_i8(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_i4(const AttnLaunch& a, hipStream_t stream);
+
+// ---- KV writers ------------------------------------------------------------
+int launch_quantize_per_token(const void* x, void* q, void* scale, long rows, int qmax,
+                              bool pack4, hipStream_t stream);
+int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int batch,
+                                     int n_kv_heads, int seqlen, int group_size,
+                                     hipStream_t stream);
+
+// ---- W4A16 -----------------------------------------------------------------
+struct GemmPlan {
+    int kind;          // 0: single-row GEMV, 1: tiled multi-row
+    int cols_per_lane; // 4 (16-byte weight loads) or 1
+    int tile_n;        // output columns per workgroup
+    int tile_m;        // output rows per workgroup
+    int n_tiles, m_tiles;
+    int splits;        // K splits
+    int kp_per_split;  // packed K rows (8 K each) per split
+    size_t workspace_bytes;
+    size_t off_part;
+};
+
+GemmPlan plan_w4a16(int M, int N, int K, int group_size);
+int launch_w4a16(const void* act, const void* w, const void* scale, void* out, bool f32_out,
+                 int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
+                 hipStream_t stream);
+int launch_w4a16_dequantize(const void* w, const void* scale, void* out, int K, int N,
+                            int group_size, hipStream_t stream);
+
+// ---- fused elementwise -----------------------------------------------------
+int launch_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps,
+                   hipStream_t stream);
+int launch_silu_mul(const void* g, const void* u, void* out, long n, hipStream_t stream);
+int launch_rope(const void* x, const void* cs, const void* sn, void* out, int B, int H, int S,
+                int D, hipStream_t stream);
+
+}  // namespace llmik

@@ -1,0 +1,456 @@
+// W4A16 (INT4 weight, fp16 activation, group-wise fp16 scales) GEMV/GEMM
+// for gfx950.
+//
+//   out[m, n] = sum_k act[m, k] * q[k, n] * scale[k / group_size, n]
+//
+// (reference/quant_matmul_ref.py:112-135; bindings/extension.cpp:322-376.)
+// weight_packed is [K/8, N] uint32: bits 4i..4i+3 of word (kp, n) hold the
+// two's-complement code of K position 8*kp + i
+// (reference/quant_matmul_ref.py:140-165).
+//
+// Split-K with a deterministic in-kernel reduction: each workgroup writes
+// its fp32 partial for its (column tile, K split) to the workspace; the last
+// workgroup of a column tile (completion counter) sums the splits in fixed
+// order and writes the output. One launch per call, no float atomics (the
+// reference accumulates split partials with atomicAdd,
+// kernels/quant/quant_matmul.cu:586-597).
+#include "device_common.hpp"
+#include "llmik_internal.hpp"
+
+namespace llmik {
+
+constexpr int kGemmThreads = 256;   // 4 waves share one column tile
+constexpr int kGemmWaves = kGemmThreads / kWave;
+
+struct GemmParams {
+    const uint16_t* act;
+    const uint32_t* w;
+    const uint16_t* scale;
+    void* out;
+    float* part;         // [splits, M, N]
+    uint32_t* counters;  // [m_tiles * n_tiles]
+    int M, N, K, group_size;
+    int splits, kp_per_split, n_tiles;
+    int f32_out;
+};
+
+// Eight int4 codes of one word -> four fp16 pairs, exact. Pair j holds the
+// codes of K positions (j, j + 4):
+//   u = code + 8 (xor 0x8 per nibble); 0x6400 | u is the fp16 value 1024 + u,
+//   and 0x6400 | (u << 4) is 1024 + 16u; subtracting / rescaling recovers
+//   the code exactly.
+__device__ __forceinline__ void i4x8_to_f16_pairs(uint32_t w, f16x2 out[4]) {
+    w ^= 0x88888888u;
+    const uint32_t w8 = w >> 8;
+    const uint32_t a = (w & 0x000F000Fu) | 0x64006400u;
+    const uint32_t b = (w & 0x00F000F0u) | 0x64006400u;
+    const uint32_t c = (w8 & 0x000F000Fu) | 0x64006400u;
+    const uint32_t d = (w8 & 0x00F000F0u) | 0x64006400u;
+    const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
+    out[0] = __builtin_bit_cast(f16x2, a) - bias;
+    out[1] = __builtin_bit_cast(f16x2, b) * sixteenth - bias16;
+    out[2] = __builtin_bit_cast(f16x2, c) - bias;
+    out[3] = __builtin_bit_cast(f16x2, d) * sixteenth - bias16;
+}
+
+// Activation pairs matching i4x8_to_f16_pairs: (a0,a4), (a1,a5), (a2,a6), (a3,a7).
+__device__ __forceinline__ void act_pairs(const u32x4 a, f16x2 out[4]) {
+    const f16x2 lo0 = __builtin_bit_cast(f16x2, a[0]);   // a0 a1
+    const f16x2 lo1 = __builtin_bit_cast(f16x2, a[1]);   // a2 a3
+    const f16x2 hi0 = __builtin_bit_cast(f16x2, a[2]);   // a4 a5
+    const f16x2 hi1 = __builtin_bit_cast(f16x2, a[3]);   // a6 a7
+    out[0] = f16x2{lo0[0], hi0[0]};
+    out[1] = f16x2{lo0[1], hi0[1]};
+    out[2] = f16x2{lo1[0], hi1[0]};
+    out[3] = f16x2{lo1[1], hi1[1]};
+}
+
+// Store the workgroup's column-tile result, or publish it as a split partial
+// and let the last split of the tile reduce. `vals[j]` belongs to column
+// n0 + j for j < count (thread-local columns), row m.
+__device__ __forceinline__ void store_out(const GemmParams& p, int m, int n, float v) {
+    if (p.f32_out) {
+        static_cast<float*>(p.out)[(long)m * p.N + n] = v;
+    } else {
+        static_cast<uint16_t*>(p.out)[(long)m * p.N + n] = f2h_bits(v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M == 1: each lane owns COLS adjacent columns (one 4*COLS-byte load per
+// packed row); the 4 waves of a workgroup cover contiguous slices of the
+// workgroup's K range and are summed in LDS.
+// ---------------------------------------------------------------------------
+template <int COLS>
+__global__ __launch_bounds__(kGemmThreads) void w4a16_gemv_kernel(GemmParams p) {
+    const int tile = blockIdx.x;
+    const int split = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = tile * (64 * COLS) + lane * COLS;
+    const bool active = n0 < p.N;
+
+    const int kp_total = p.K / 8;
+    const int kp_split0 = split * p.kp_per_split;
+    const int kp_split1 = min(kp_split0 + p.kp_per_split, kp_total);
+    const int per_wave = (p.kp_per_split + kGemmWaves - 1) / kGemmWaves;
+    const int kp0 = min(kp_split0 + wave * per_wave, kp_split1);
+    const int kp1 = min(kp0 + per_wave, kp_split1);
+    const int kp_per_group = p.group_size / 8;
+
+    float acc[COLS], accg[COLS];
+#pragma unroll
+    for (int j = 0; j < COLS; ++j) acc[j] = accg[j] = 0.0f;
+    int g_cur = kp0 / kp_per_group;
+
+    for (int kp = kp0; kp < kp1; ++kp) {
+        const int g = kp / kp_per_group;
+        if (g != g_cur) {
+            if (active) {
+#pragma unroll
+                for (int j = 0; j < COLS; ++j) {
+                    acc[j] = fmaf(h2f(p.scale[(long)g_cur * p.N + n0 + j]), accg[j], acc[j]);
+                    accg[j] = 0.0f;
+                }
+            }
+            g_cur = g;
+        }
+        f16x2 ap[4];
+        act_pairs(load16(p.act + 8 * kp), ap);
+        if (active) {
+            uint32_t wv[COLS];
+            if constexpr (COLS == 4) {
+                const u32x4 raw = load16(p.w + (long)kp * p.N + n0);
+                wv[0] = raw[0]; wv[1] = raw[1]; wv[2] = raw[2]; wv[3] = raw[3];
+            } else {
+                wv[0] = p.w[(long)kp * p.N + n0];
+            }
+#pragma unroll
+            for (int j = 0; j < COLS; ++j) {
+                f16x2 wp[4];
+                i4x8_to_f16_pairs(wv[j], wp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) accg[j] = __builtin_amdgcn_fdot2(ap[i], wp[i], accg[j], false);
+            }
+        }
+    }
+    if (active && kp0 < kp1) {
+#pragma unroll
+        for (int j = 0; j < COLS; ++j)
+            acc[j] = fmaf(h2f(p.scale[(long)g_cur * p.N + n0 + j]), accg[j], acc[j]);
+    }
+
+    __shared__ float s_part[kGemmWaves][64 * COLS];
+    __shared__ uint32_t s_last;
+#pragma unroll
+    for (int j = 0; j < COLS; ++j) s_part[wave][lane * COLS + j] = acc[j];
+    __syncthreads();
+
+    const int tile_n = 64 * COLS;
+    const int nbase = tile * tile_n;
+    float tot[(64 * COLS + kGemmThreads - 1) / kGemmThreads];
+#pragma unroll
+    for (int i = 0; i < (64 * COLS + kGemmThreads - 1) / kGemmThreads; ++i) {
+        const int col = threadIdx.x + i * kGemmThreads;
+        tot[i] = 0.0f;
+        if (col < tile_n) {
+#pragma unroll
+            for (int w = 0; w < kGemmWaves; ++w) tot[i] += s_part[w][col];
+        }
+    }
+
+    if (p.splits == 1) {
+#pragma unroll
+        for (int i = 0; i < (64 * COLS + kGemmThreads - 1) / kGemmThreads; ++i) {
+            const int col = threadIdx.x + i * kGemmThreads;
+            if (col < tile_n && nbase + col < p.N) store_out(p, 0, nbase + col, tot[i]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < (64 * COLS + kGemmThreads - 1) / kGemmThreads; ++i) {
+        const int col = threadIdx.x + i * kGemmThreads;
+        if (col < tile_n && nbase + col < p.N) p.part[(long)split * p.N + nbase + col] = tot[i];
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(&p.counters[tile], 1u);
+        s_last = (prev == (uint32_t)(p.splits - 1)) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_last == 0u) return;
+    __threadfence();
+#pragma unroll
+    for (int i = 0; i < (64 * COLS + kGemmThreads - 1) / kGemmThreads; ++i) {
+        const int col = threadIdx.x + i * kGemmThreads;
+        if (col < tile_n && nbase + col < p.N) {
+            float v = 0.0f;
+            for (int sp = 0; sp < p.splits; ++sp) v += p.part[(long)sp * p.N + nbase + col];
+            store_out(p, 0, nbase + col, v);
+        }
+    }
+    if (threadIdx.x == 0) p.counters[tile] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// M > 1: each lane owns COLS columns and MT rows; the weight is dequantised
+// once per packed word into fp32 (code * scale, exact) and reused across the
+// MT rows. Grid z walks the row tiles.
+// ---------------------------------------------------------------------------
+template <int COLS, int MT>
+__global__ __launch_bounds__(kGemmThreads) void w4a16_gemm_tiled_kernel(GemmParams p) {
+    const int tile = blockIdx.x;
+    const int split = blockIdx.y;
+    const int mtile = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = tile * (64 * COLS) + lane * COLS;
+    const bool active = n0 < p.N;
+    const int m0 = mtile * MT;
+    const int mrows = min(MT, p.M - m0);
+
+    const int kp_total = p.K / 8;
+    const int kp_split0 = split * p.kp_per_split;
+    const int kp_split1 = min(kp_split0 + p.kp_per_split, kp_total);
+    const int per_wave = (p.kp_per_split + kGemmWaves - 1) / kGemmWaves;
+    const int kp0 = min(kp_split0 + wave * per_wave, kp_split1);
+    const int kp1 = min(kp0 + per_wave, kp_split1);
+    const int kp_per_group = p.group_size / 8;
+
+    float acc[MT][COLS];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < COLS; ++j) acc[m][j] = 0.0f;
+
+    for (int kp = kp0; kp < kp1; ++kp) {
+        const int g = kp / kp_per_group;
+        float wf[COLS][8];
+        if (active) {
+#pragma unroll
+            for (int j = 0; j < COLS; ++j) {
+                const float s = h2f(p.scale[(long)g * p.N + n0 + j]);
+                float codes[8];
+                i4x8_to_f32(p.w[(long)kp * p.N + n0 + j], codes);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) wf[j][e] = codes[e] * s;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < COLS; ++j)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) wf[j][e] = 0.0f;
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m < mrows) {
+                float a[8];
+                f16x8_to_f32(load16(p.act + (long)(m0 + m) * p.K + 8 * kp), a);
+#pragma unroll
+                for (int j = 0; j < COLS; ++j)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[m][j] = fmaf(a[e], wf[j][e], acc[m][j]);
+            }
+        }
+    }
+
+    __shared__ float s_part[kGemmWaves][MT][64 * COLS];
+    __shared__ uint32_t s_last;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < COLS; ++j) s_part[wave][m][lane * COLS + j] = acc[m][j];
+    __syncthreads();
+
+    const int tile_n = 64 * COLS;
+    const int nbase = tile * tile_n;
+    const int outs = MT * tile_n;
+    constexpr int kPer = (MT * 64 * COLS + kGemmThreads - 1) / kGemmThreads;
+    float tot[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = threadIdx.x + i * kGemmThreads;
+        tot[i] = 0.0f;
+        if (idx < outs) {
+            const int m = idx / tile_n, col = idx % tile_n;
+#pragma unroll
+            for (int w = 0; w < kGemmWaves; ++w) tot[i] += s_part[w][m][col];
+        }
+    }
+    const int counter = mtile * p.n_tiles + tile;
+    if (p.splits == 1) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = threadIdx.x + i * kGemmThreads;
+            const int m = idx / tile_n, col = idx % tile_n;
+            if (idx < outs && m < mrows && nbase + col < p.N) store_out(p, m0 + m, nbase + col, tot[i]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = threadIdx.x + i * kGemmThreads;
+        const int m = idx / tile_n, col = idx % tile_n;
+        if (idx < outs && m < mrows && nbase + col < p.N)
+            p.part[((long)split * p.M + m0 + m) * p.N + nbase + col] = tot[i];
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(&p.counters[counter], 1u);
+        s_last = (prev == (uint32_t)(p.splits - 1)) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_last == 0u) return;
+    __threadfence();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = threadIdx.x + i * kGemmThreads;
+        const int m = idx / tile_n, col = idx % tile_n;
+        if (idx < outs && m < mrows && nbase + col < p.N) {
+            float v = 0.0f;
+            for (int sp = 0; sp < p.splits; ++sp)
+                v += p.part[((long)sp * p.M + m0 + m) * p.N + nbase + col];
+            store_out(p, m0 + m, nbase + col, v);
+        }
+    }
+    if (threadIdx.x == 0) p.counters[counter] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Dequantise: one thread per (packed row, 4 columns) -> 8 rows x 4 fp16.
+// W[k, n] = fp16(code * scale) with the product exact in fp32
+// (kernels/quant/quant_matmul.cu:612-627 semantics).
+// ---------------------------------------------------------------------------
+template <int COLS>
+__global__ __launch_bounds__(256) void w4a16_dequantize_kernel(const uint32_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ scale,
+                                                               uint16_t* __restrict__ out, int K,
+                                                               int N, int group_size) {
+    const int n0 = (blockIdx.x * 256 + threadIdx.x) * COLS;
+    const int kp = blockIdx.y;
+    if (n0 >= N) return;
+    const int g = (kp * 8) / group_size;
+    float codes[COLS][8];
+    float s[COLS];
+    if constexpr (COLS == 4) {
+        const u32x4 raw = load16(w + (long)kp * N + n0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) i4x8_to_f32(raw[j], codes[j]);
+        const u32x2 sr = load8(scale + (long)g * N + n0);
+        s[0] = h2f(sr[0] & 0xFFFF); s[1] = h2f(sr[0] >> 16);
+        s[2] = h2f(sr[1] & 0xFFFF); s[3] = h2f(sr[1] >> 16);
+    } else {
+        i4x8_to_f32(w[(long)kp * N + n0], codes[0]);
+        s[0] = h2f(scale[(long)g * N + n0]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        uint16_t* dst = out + (long)(kp * 8 + e) * N + n0;
+        if constexpr (COLS == 4) {
+            u32x2 v;
+            v[0] = (uint32_t)f2h_bits(codes[0][e] * s[0]) | ((uint32_t)f2h_bits(codes[1][e] * s[1]) << 16);
+            v[1] = (uint32_t)f2h_bits(codes[2][e] * s[2]) | ((uint32_t)f2h_bits(codes[3][e] * s[3]) << 16);
+            *reinterpret_cast<u32x2*>(dst) = v;
+        } else {
+            dst[0] = f2h_bits(codes[0][e] * s[0]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
+    GemmPlan pl{};
+    pl.cols_per_lane = (N % 4 == 0) ? 4 : 1;
+    pl.tile_n = 64 * pl.cols_per_lane;
+    pl.n_tiles = (N + pl.tile_n - 1) / pl.tile_n;
+    pl.kind = (M == 1) ? 0 : 1;
+    pl.tile_m = (M == 1) ? 1 : (M <= 4 ? 4 : (M <= 8 ? 8 : 16));
+    if (pl.kind == 1 && pl.cols_per_lane == 4 && pl.tile_m > 8) pl.tile_m = 8;
+    pl.m_tiles = (M + pl.tile_m - 1) / pl.tile_m;
+    const int kp_total = K / 8;
+    const int cus = device_cu_count();
+    const long base = (long)pl.n_tiles * pl.m_tiles;
+    // Target ~2 workgroups per CU; keep >= 4 packed rows per wave.
+    long want = (2L * cus + base - 1) / base;
+    const long max_splits = (kp_total + 4 * kGemmWaves - 1) / (4 * kGemmWaves);
+    if (want > max_splits) want = max_splits;
+    if (want < 1) want = 1;
+    int kps = (int)((kp_total + want - 1) / want);
+    kps = (kps + kGemmWaves - 1) / kGemmWaves * kGemmWaves;
+    pl.kp_per_split = kps;
+    pl.splits = (kp_total + kps - 1) / kps;
+    const size_t counters = align_up((size_t)base * sizeof(uint32_t), 256);
+    const size_t part = align_up((size_t)pl.splits * M * N * sizeof(float), 256);
+    pl.off_part = counters;
+    pl.workspace_bytes = (pl.splits > 1) ? counters + part : 0;
+    return pl;
+}
+
+int launch_w4a16(const void* act, const void* w, const void* scale, void* out, bool f32_out,
+                 int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
+                 hipStream_t stream) {
+    if (M == 0 || N == 0) return LLMIK_OK;
+    const GemmPlan pl = plan_w4a16(M, N, K, group_size);
+    if (pl.splits > 1 && ws_bytes < pl.workspace_bytes)
+        return set_error(LLMIK_ERR_WORKSPACE, "workspace too small for this W4A16 call");
+    if (pl.m_tiles > 65535 || pl.splits > 65535)
+        return set_error(LLMIK_ERR_UNSUPPORTED, "W4A16 grid too large");
+    GemmParams p{};
+    p.act = static_cast<const uint16_t*>(act);
+    p.w = static_cast<const uint32_t*>(w);
+    p.scale = static_cast<const uint16_t*>(scale);
+    p.out = out;
+    char* wsp = static_cast<char*>(ws);
+    p.counters = reinterpret_cast<uint32_t*>(wsp);
+    p.part = wsp ? reinterpret_cast<float*>(wsp + pl.off_part) : nullptr;
+    p.M = M; p.N = N; p.K = K; p.group_size = group_size;
+    p.splits = pl.splits;
+    p.kp_per_split = pl.kp_per_split;
+    p.n_tiles = pl.n_tiles;
+    p.f32_out = f32_out ? 1 : 0;
+    dim3 block(kGemmThreads);
+    if (pl.kind == 0) {
+        dim3 grid(pl.n_tiles, pl.splits);
+        if (pl.cols_per_lane == 4) hipLaunchKernelGGL(w4a16_gemv_kernel<4>, grid, block, 0, stream, p);
+        else hipLaunchKernelGGL(w4a16_gemv_kernel<1>, grid, block, 0, stream, p);
+    } else {
+        dim3 grid(pl.n_tiles, pl.splits, pl.m_tiles);
+        if (pl.cols_per_lane == 4) {
+            if (pl.tile_m == 4) hipLaunchKernelGGL((w4a16_gemm_tiled_kernel<4, 4>), grid, block, 0, stream, p);
+            else hipLaunchKernelGGL((w4a16_gemm_tiled_kernel<4, 8>), grid, block, 0, stream, p);
+        } else {
+            if (pl.tile_m == 4) hipLaunchKernelGGL((w4a16_gemm_tiled_kernel<1, 4>), grid, block, 0, stream, p);
+            else if (pl.tile_m == 8) hipLaunchKernelGGL((w4a16_gemm_tiled_kernel<1, 8>), grid, block, 0, stream, p);
+            else hipLaunchKernelGGL((w4a16_gemm_tiled_kernel<1, 16>), grid, block, 0, stream, p);
+        }
+    }
+    return check_launch();
+}
+
+int launch_w4a16_dequantize(const void* w, const void* scale, void* out, int K, int N,
+                            int group_size, hipStream_t stream) {
+    if (K == 0 || N == 0) return LLMIK_OK;
+    const int kp_total = K / 8;
+    if (kp_total > 65535) return set_error(LLMIK_ERR_UNSUPPORTED, "K/8 exceeds 65535");
+    if (N % 4 == 0) {
+        dim3 grid((N / 4 + 255) / 256, kp_total);
+        hipLaunchKernelGGL(w4a16_dequantize_kernel<4>, grid, dim3(256), 0, stream,
+                           static_cast<const uint32_t*>(w), static_cast<const uint16_t*>(scale),
+                           static_cast<uint16_t*>(out), K, N, group_size);
+    } else {
+        dim3 grid((N + 255) / 256, kp_total);
+        hipLaunchKernelGGL(w4a16_dequantize_kernel<1>, grid, dim3(256), 0, stream,
+                           static_cast<const uint32_t*>(w), static_cast<const uint16_t*>(scale),
+                           static_cast<uint16_t*>(out), K, N, group_size);
+    }
+    return check_launch();
+}
+
+}  // namespace llmik

@@ -1,0 +1,66 @@
+"""Loader and ctypes signatures for libllmik_hip.so (include/llmik.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already mapped (both carry the soname libamdhip64.so.7). A missing library
+is an ImportError: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime first)
+
+LIB_PATH = Path(os.environ.get("LLMIK_LIB", Path(__file__).resolve().parent / "libllmik_hip.so"))
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"llmik_cuda: {LIB_PATH} is missing. Build it with "
+        "`python llm-inference-kernels_amd/build_lib.py` (or __graft_entry__.build()).")
+
+lib = ctypes.CDLL(str(LIB_PATH))
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+_l = ctypes.c_long
+
+_SIGNATURES = {
+    "llmik_last_error": (ctypes.c_char_p, []),
+    "llmik_abi_version": (_i, []),
+    "llmik_attention_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
+    "llmik_decode_attention_f16": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p]),
+    "llmik_decode_attention_int8": (
+        _i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p]),
+    "llmik_decode_attention_int4": (
+        _i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p]),
+    "llmik_quantize_per_token_int8": (_i, [_p, _p, _p, _i, _i, _i, _i, _p]),
+    "llmik_quantize_k_per_channel_groupwise_int4": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _p]),
+    "llmik_quantize_v_per_token_int4": (_i, [_p, _p, _p, _i, _i, _i, _i, _p]),
+    "llmik_w4a16_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "llmik_w4a16_gemm": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
+    "llmik_w4a16_gemm_f32out": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
+    "llmik_w4a16_dequantize": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "llmik_rmsnorm": (_i, [_p, _p, _p, _i, _i, _f, _p]),
+    "llmik_silu_mul": (_i, [_p, _p, _p, _l, _p]),
+    "llmik_rope": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
+}
+
+for _name, (_res, _args) in _SIGNATURES.items():
+    _fn = getattr(lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+ABI_VERSION = 1
+if lib.llmik_abi_version() != ABI_VERSION:
+    raise ImportError(f"llmik_cuda: {LIB_PATH} has ABI {lib.llmik_abi_version()}, "
+                      f"expected {ABI_VERSION}; rebuild it")
+
+
+def check(status: int) -> None:
+    """Raise RuntimeError for a non-zero llmik_status."""
+    if status != 0:
+        msg = lib.llmik_last_error().decode(errors="replace")
+        raise RuntimeError(f"llmik: {msg} (status {status})")

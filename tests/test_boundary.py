@@ -1,0 +1,209 @@
+"""The C ABI boundary and the llmik_cuda host layer, on the CPU.
+
+* libllmik_hip.so loads and exports every entry point include/llmik.h
+  declares, with the ABI version the host layer expects;
+* the C layer rejects bad arguments with LLMIK_ERR_* codes and messages
+  before touching the GPU (null / misaligned pointers, head_dim != 128,
+  seqlen > kv_buf_len, K / group_size rules);
+* the Python layer raises RuntimeError with the reference binding's
+  TORCH_CHECK messages (bindings/extension.cpp), for every validation path
+  the reference has, without launching anything;
+* the op surface has the reference's names, argument order and defaults.
+No test here calls a compute entry point with valid arguments.
+"""
+from __future__ import annotations
+
+import ctypes
+import inspect
+import re
+
+import pytest
+import torch
+
+from tests.helpers import ROOT
+
+HEADER = ROOT / "include" / "llmik.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"LLMIK_API\s+[\w\s\*]+?\b(llmik_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def mod():
+    import llmik_cuda
+    return llmik_cuda
+
+
+@pytest.fixture(scope="module")
+def lib(mod):
+    from llmik_cuda._lib import lib
+    return lib
+
+
+def test_header_declares_expected_entry_points():
+    syms = declared_symbols()
+    for name in ["llmik_decode_attention_f16", "llmik_decode_attention_int8",
+                 "llmik_decode_attention_int4", "llmik_quantize_per_token_int8",
+                 "llmik_quantize_k_per_channel_groupwise_int4", "llmik_quantize_v_per_token_int4",
+                 "llmik_w4a16_gemm", "llmik_w4a16_dequantize", "llmik_rmsnorm", "llmik_silu_mul",
+                 "llmik_rope", "llmik_attention_workspace_size", "llmik_w4a16_workspace_size"]:
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.llmik_abi_version() == 1
+
+
+def test_library_was_built_for_gfx950_only():
+    from llmik_cuda._lib import LIB_PATH
+    data = LIB_PATH.read_bytes()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in data
+
+
+def _err(lib):
+    return lib.llmik_last_error().decode()
+
+
+def test_c_layer_argument_errors(lib):
+    S = None
+    st = lib.llmik_decode_attention_f16(16, 16, 16, 16, 1, 32, 8, 10, 64, 10, 1.0, None, 0, S)
+    assert st == -1 and "head_dim=128" in _err(lib)
+    st = lib.llmik_decode_attention_f16(16, 16, 16, 16, 1, 32, 8, 11, 128, 10, 1.0, None, 0, S)
+    assert st == -1 and "seqlen exceeds" in _err(lib)
+    st = lib.llmik_decode_attention_f16(16, 16, 16, 16, 1, 30, 8, 10, 128, 10, 1.0, None, 0, S)
+    assert st == -1 and "multiple of n_kv_heads" in _err(lib)
+    st = lib.llmik_decode_attention_f16(17, 16, 16, 16, 1, 32, 8, 10, 128, 10, 1.0, None, 0, S)
+    assert st == -4
+    st = lib.llmik_decode_attention_int4(16, 16, 16, 16, 16, 16, 1, 32, 8, 100, 128, 100, 32, 3,
+                                         1.0, None, 0, S)
+    assert st == -1 and "fewer groups" in _err(lib)
+    st = lib.llmik_quantize_per_token_int8(16, 16, 16, 1, 8, 4, 64, S)
+    assert st == -1 and "head_dim=128" in _err(lib)
+    st = lib.llmik_quantize_k_per_channel_groupwise_int4(16, 16, 16, 1, 8, 4, 128, 0, S)
+    assert st == -1 and "group_size must be positive" in _err(lib)
+    st = lib.llmik_w4a16_gemm(16, 16, 16, 16, 1, 64, 100, 100, None, 0, S)
+    assert st == -1 and "K_packs * 8" in _err(lib)
+    st = lib.llmik_w4a16_gemm(16, 16, 16, 16, 1, 64, 128, 12, None, 0, S)
+    assert st == -1 and "multiple of 8" in _err(lib)
+    st = lib.llmik_w4a16_gemm(16, 16, 16, 16, 1, 64, 128, 48, None, 0, S)
+    assert st == -1 and "n_groups * group_size" in _err(lib)
+    st = lib.llmik_rope(16, 16, 16, 16, 1, 1, 1, 7, S)
+    assert st == -1 and "even" in _err(lib)
+
+
+def test_workspace_sizes_without_gpu(lib):
+    assert lib.llmik_attention_workspace_size(8, 32, 8, 4096, 128) > 0
+    assert lib.llmik_attention_workspace_size(8, 32, 8, 4096, 64) == 0
+    assert lib.llmik_w4a16_workspace_size(1, 4096, 4096, 128) > 0
+
+
+def test_op_surface_matches_reference(mod):
+    expect = {
+        "decode_attention": ["q", "k", "v", "softmax_scale", "seqlen"],
+        "decode_attention_v3": ["q", "k", "v", "softmax_scale"],
+        "quantize_per_token": ["x"],
+        "decode_attention_int8": ["q", "k_q", "k_scale", "v_q", "v_scale", "softmax_scale"],
+        "quantize_k_per_channel_groupwise_int4": ["x", "group_size"],
+        "quantize_v_per_token_int4": ["x"],
+        "decode_attention_int4": ["q", "k_q", "k_scale", "v_q", "v_scale", "group_size",
+                                  "softmax_scale"],
+        "w4a16_gemm": ["act", "weight_packed", "scale", "group_size"],
+        "w4a16_dequantize": ["weight_packed", "scale", "group_size"],
+        "rmsnorm": ["x", "weight", "eps"],
+        "silu_mul": ["gate", "up"],
+        "rope": ["x", "cos", "sin"],
+    }
+    for name, params in expect.items():
+        sig = inspect.signature(getattr(mod, name))
+        got = list(sig.parameters)
+        assert got[:len(params)] == params, name
+        for extra in got[len(params):]:
+            assert sig.parameters[extra].default is not inspect.Parameter.empty, (name, extra)
+    assert inspect.signature(mod.decode_attention).parameters["seqlen"].default == -1
+
+
+H16 = torch.float16
+
+
+def _t(*shape, dtype=H16):
+    return torch.zeros(*shape, dtype=dtype)
+
+
+@pytest.fixture
+def as_device(mod, monkeypatch):
+    """Treat CPU tensors as device tensors so the later checks are reachable;
+    every case below must raise before any launch."""
+    monkeypatch.setattr(mod, "_is_device", lambda t: True)
+    return mod
+
+
+def test_python_checks_device_first(mod):
+    with pytest.raises(RuntimeError, match="q, k, v must be CUDA tensors"):
+        mod.decode_attention(_t(1, 32, 128), _t(1, 8, 4, 128), _t(1, 8, 4, 128), 0.1)
+    with pytest.raises(RuntimeError, match="x must be CUDA"):
+        mod.quantize_per_token(_t(1, 8, 4, 128))
+    with pytest.raises(RuntimeError, match="all inputs must be CUDA tensors"):
+        mod.w4a16_gemm(_t(1, 64), _t(8, 16, dtype=torch.int32), _t(1, 16), 64)
+
+
+@pytest.mark.parametrize("case", [
+    ("decode_attention", lambda m: m.decode_attention(_t(1, 32, 128, dtype=torch.float32),
+                                                      _t(1, 8, 4, 128), _t(1, 8, 4, 128), 0.1),
+     "fp16 only for now"),
+    ("decode_attention", lambda m: m.decode_attention(_t(1, 32, 128), _t(1, 8, 4, 128).transpose(2, 3),
+                                                      _t(1, 8, 4, 128), 0.1),
+     "inputs must be contiguous"),
+    ("decode_attention", lambda m: m.decode_attention(_t(1, 32, 128), _t(1, 8, 4, 128),
+                                                      _t(1, 8, 4, 128), 0.1, 5),
+     "seqlen exceeds allocated cache length"),
+    ("quantize_per_token", lambda m: m.quantize_per_token(_t(1, 8, 4, 128, dtype=torch.float32)),
+     "x must be fp16"),
+    ("quantize_per_token", lambda m: m.quantize_per_token(_t(8, 4, 128)),
+     r"x must be \[batch, n_kv_heads, seqlen, head_dim\]"),
+    ("quantize_per_token", lambda m: m.quantize_per_token(_t(1, 8, 4, 64)),
+     "only head_dim=128 supported"),
+    ("quantize_k", lambda m: m.quantize_k_per_channel_groupwise_int4(_t(1, 8, 4, 128), 0),
+     "group_size must be positive"),
+    ("quantize_v", lambda m: m.quantize_v_per_token_int4(_t(1, 8, 4, 128)[:, :, :, ::2]),
+     "x must be contiguous"),
+    ("int8", lambda m: m.decode_attention_int8(_t(1, 32, 128), _t(1, 8, 4, 128), _t(1, 8, 4),
+                                               _t(1, 8, 4, 128), _t(1, 8, 4), 0.1),
+     "k_q and v_q must be int8"),
+    ("int8", lambda m: m.decode_attention_int8(_t(1, 32, 128), _t(1, 8, 4, 128, dtype=torch.int8),
+                                               _t(1, 8, 4, dtype=torch.float32),
+                                               _t(1, 8, 4, 128, dtype=torch.int8), _t(1, 8, 4), 0.1),
+     "k_scale and v_scale must be fp16"),
+    ("int4", lambda m: m.decode_attention_int4(_t(1, 32, 128), _t(1, 8, 4, 64),
+                                               _t(1, 8, 1, 128), _t(1, 8, 4, 64), _t(1, 8, 4), 32, 0.1),
+     r"k_q and v_q must be int8 \(packed int4\)"),
+    ("gemm", lambda m: m.w4a16_gemm(_t(1, 64, dtype=torch.float32), _t(8, 16, dtype=torch.int32),
+                                    _t(1, 16), 64), "act must be fp16"),
+    ("gemm", lambda m: m.w4a16_gemm(_t(1, 64), _t(8, 16), _t(1, 16), 64),
+     r"weight_packed must be int32 \(uint32 bit pattern\)"),
+    ("gemm", lambda m: m.w4a16_gemm(_t(1, 72), _t(8, 16, dtype=torch.int32), _t(1, 16), 64),
+     "act.K must equal weight_packed.K_packs"),
+    ("gemm", lambda m: m.w4a16_gemm(_t(1, 64), _t(8, 16, dtype=torch.int32), _t(1, 8), 64),
+     "scale and weight_packed N mismatch"),
+    ("gemm", lambda m: m.w4a16_gemm(_t(1, 64), _t(8, 16, dtype=torch.int32), _t(1, 16), 12),
+     "group_size must be a positive multiple of 8"),
+    ("gemm", lambda m: m.w4a16_gemm(_t(1, 64), _t(8, 16, dtype=torch.int32), _t(2, 16), 64),
+     "K must equal n_groups \\* group_size"),
+    ("gemm", lambda m: m.w4a16_gemm(_t(64), _t(8, 16, dtype=torch.int32), _t(1, 16), 64),
+     "all inputs must be 2D"),
+    ("dequant", lambda m: m.w4a16_dequantize(_t(8, 16, dtype=torch.int32), _t(1, 16), 48),
+     "K must be a multiple of group_size"),
+    ("rmsnorm", lambda m: m.rmsnorm(_t(2, 64), _t(32), 1e-5), "weight length must match"),
+    ("silu", lambda m: m.silu_mul(_t(2, 64), _t(2, 32)), "gate and up must have the same shape"),
+    ("rope", lambda m: m.rope(_t(2, 4, 1, 7), _t(2, 1, 7), _t(2, 1, 7)), "head_dim must be even"),
+    ("rope", lambda m: m.rope(_t(2, 4, 3, 8), _t(2, 8), _t(2, 8)), "cos/sin must be"),
+])
+def test_python_validation_messages(as_device, case):
+    _, call, msg = case
+    with pytest.raises(RuntimeError, match=msg):
+        call(as_device)

@@ -1,0 +1,157 @@
+"""GPU parity: split-K decode attention (fp16, INT8, INT4 KIVI) vs the
+oracle, max-abs <= 2e-3 against the fp32 oracle on the same inputs.
+
+INT8 / INT4 cases quantise with this build's writers (whose codes and scales
+are checked bit-exact in test_gpu_kv_writers.py) and compare against the
+oracle run on the fp32-dequantised cache, so the gate isolates the fused
+dequant + attention arithmetic.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import kv_quant as kq
+from tests.helpers import kv_with_outliers, randn
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _inputs(B, H, Hkv, L, seed, outliers=False):
+    q = randn((B, H, 128), seed).astype(np.float16)
+    k = (kv_with_outliers((B, Hkv, L, 128), seed + 1) if outliers
+         else randn((B, Hkv, L, 128), seed + 1)).astype(np.float16)
+    v = randn((B, Hkv, L, 128), seed + 2).astype(np.float16)
+    return q, k, v
+
+
+def _max_abs(out: torch.Tensor, ref: np.ndarray) -> float:
+    return float(np.abs(out.float().cpu().numpy() - ref).max())
+
+
+@pytest.mark.parametrize("B,H,Hkv,L", [
+    (1, 32, 8, 512),      # CPU-plumbing config shape
+    (8, 32, 8, 4096),     # headline config
+    (1, 32, 8, 1), (2, 32, 8, 17), (1, 32, 8, 100), (8, 32, 8, 1024), (1, 32, 8, 16384),
+    (3, 8, 8, 300),       # MHA
+    (2, 16, 8, 777),      # GQA 2
+    (2, 12, 4, 257),      # GQA 3
+    (1, 64, 8, 2048),     # GQA 8 (two head chunks per kv head)
+])
+def test_fp16_matches_oracle(llmik, cuda, B, H, Hkv, L):
+    q, k, v = _inputs(B, H, Hkv, L, seed=B * 1000 + L)
+    scale = 1.0 / math.sqrt(128)
+    out = llmik.decode_attention(_dev(q, cuda), _dev(k, cuda), _dev(v, cuda), scale)
+    torch.cuda.synchronize()
+    assert out.shape == (B, H, 128) and out.dtype == torch.float16
+    ref = oa.decode_attention(q, k, v, scale)
+    assert _max_abs(out, ref) <= TOL
+
+
+def test_fp16_v3_alias_and_named_args(llmik, cuda):
+    q, k, v = _inputs(2, 32, 8, 333, seed=7)
+    qd, kd, vd = _dev(q, cuda), _dev(k, cuda), _dev(v, cuda)
+    a = llmik.decode_attention(q=qd, k=kd, v=vd, softmax_scale=0.125)
+    b = llmik.decode_attention_v3(qd, kd, vd, 0.125)
+    assert torch.equal(a, b)
+    assert _max_abs(a, oa.decode_attention(q, k, v, 0.125)) <= TOL
+
+
+@pytest.mark.parametrize("buf,live", [(1024, 777), (4096, 2049), (256, 1), (512, 512)])
+def test_fp16_live_length_in_preallocated_cache(llmik, cuda, buf, live):
+    q, k, v = _inputs(2, 32, 8, buf, seed=buf + live)
+    # poison the dead tail: it must not be read
+    k[:, :, live:] = np.float16(60000.0)
+    v[:, :, live:] = np.float16(np.nan)
+    out = llmik.decode_attention(_dev(q, cuda), _dev(k, cuda), _dev(v, cuda), 0.0883883, live)
+    ref = oa.decode_attention(q, k, v, 0.0883883, seqlen=live)
+    assert _max_abs(out, ref) <= TOL
+
+
+def test_fp16_empty_cache_gives_zeros(llmik, cuda):
+    q = _dev(randn((2, 32, 128), 1).astype(np.float16), cuda)
+    k = torch.zeros((2, 8, 0, 128), dtype=torch.float16, device=cuda)
+    out = llmik.decode_attention(q, k, k.clone(), 0.1)
+    assert torch.count_nonzero(out) == 0
+
+
+def test_fp16_deterministic_across_calls(llmik, cuda):
+    q, k, v = _inputs(8, 32, 8, 4096, seed=99)
+    qd, kd, vd = _dev(q, cuda), _dev(k, cuda), _dev(v, cuda)
+    a = llmik.decode_attention(qd, kd, vd, 0.0883883)
+    for _ in range(3):
+        assert torch.equal(a, llmik.decode_attention(qd, kd, vd, 0.0883883))
+
+
+@pytest.mark.parametrize("B,L", [(1, 128), (4, 1000), (8, 4096), (1, 16384)])
+def test_int8_pipeline_matches_oracle(llmik, cuda, B, L):
+    q, k, v = _inputs(B, 32, 8, L, seed=3 * L + B, outliers=True)
+    kq_, ks = llmik.quantize_per_token(_dev(k, cuda))
+    vq_, vs = llmik.quantize_per_token(_dev(v, cuda))
+    out = llmik.decode_attention_int8(_dev(q, cuda), kq_, ks, vq_, vs, 1 / math.sqrt(128))
+    k_dq = kq.dequantize_per_token(kq_.cpu().numpy(), ks.cpu().numpy())
+    v_dq = kq.dequantize_per_token(vq_.cpu().numpy(), vs.cpu().numpy())
+    ref = oa.decode_attention(q, k_dq, v_dq, 1 / math.sqrt(128))
+    assert _max_abs(out, ref) <= TOL
+
+
+def test_int8_live_length(llmik, cuda):
+    q, k, v = _inputs(2, 32, 8, 1024, seed=5, outliers=True)
+    kq_, ks = llmik.quantize_per_token(_dev(k, cuda))
+    vq_, vs = llmik.quantize_per_token(_dev(v, cuda))
+    out = llmik.decode_attention_int8(_dev(q, cuda), kq_, ks, vq_, vs, 0.0883883, seqlen=700)
+    k_dq = kq.dequantize_per_token(kq_.cpu().numpy(), ks.cpu().numpy())
+    v_dq = kq.dequantize_per_token(vq_.cpu().numpy(), vs.cpu().numpy())
+    assert _max_abs(out, oa.decode_attention(q, k_dq, v_dq, 0.0883883, seqlen=700)) <= TOL
+
+
+@pytest.mark.parametrize("B,L,gs", [(1, 128, 32), (4, 1000, 32), (8, 4096, 128), (2, 100, 128),
+                                    (8, 2048, 32), (1, 300, 64)])
+def test_int4_pipeline_matches_oracle(llmik, cuda, B, L, gs):
+    q, k, v = _inputs(B, 32, 8, L, seed=7 * L + gs, outliers=True)
+    kq_, ks = llmik.quantize_k_per_channel_groupwise_int4(_dev(k, cuda), gs)
+    vq_, vs = llmik.quantize_v_per_token_int4(_dev(v, cuda))
+    out = llmik.decode_attention_int4(_dev(q, cuda), kq_, ks, vq_, vs, gs, 1 / math.sqrt(128))
+    k_dq = kq.dequantize_per_channel_groupwise(kq.unpack_kv_int4(kq_.cpu().numpy()),
+                                               ks.cpu().numpy(), gs)
+    v_dq = kq.dequantize_per_token(kq.unpack_kv_int4(vq_.cpu().numpy()), vs.cpu().numpy())
+    ref = oa.decode_attention(q, k_dq, v_dq, 1 / math.sqrt(128))
+    assert _max_abs(out, ref) <= TOL
+
+
+def test_int4_large_batch_config_properties(llmik, cuda):
+    """B=64, S=8192 (the second INT4 config): parity on a sample of batches
+    (the oracle is run per batch row) and a batch-permutation property."""
+    B, L, gs = 64, 8192, 128
+    gen = torch.Generator(device=cuda).manual_seed(64)
+    kd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    kd[..., [3, 37, 71, 105]] *= 10
+    vd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    kq_, ks = llmik.quantize_k_per_channel_groupwise_int4(kd, gs)
+    vq_, vs = llmik.quantize_v_per_token_int4(vd)
+    del kd, vd
+    q = randn((B, 32, 128), 65).astype(np.float16)
+    qd = _dev(q, cuda)
+    out = llmik.decode_attention_int4(qd, kq_, ks, vq_, vs, gs, 1 / math.sqrt(128))
+    for b in (0, 17, 63):
+        k_dq = kq.dequantize_per_channel_groupwise(
+            kq.unpack_kv_int4(kq_[b:b + 1].cpu().numpy()), ks[b:b + 1].cpu().numpy(), gs)
+        v_dq = kq.dequantize_per_token(kq.unpack_kv_int4(vq_[b:b + 1].cpu().numpy()),
+                                       vs[b:b + 1].cpu().numpy())
+        ref = oa.decode_attention(q[b:b + 1], k_dq, v_dq, 1 / math.sqrt(128))
+        assert _max_abs(out[b:b + 1], ref) <= TOL
+    perm = torch.randperm(B, generator=torch.Generator().manual_seed(0)).to(cuda)
+    out_p = llmik.decode_attention_int4(qd[perm].contiguous(), kq_[perm].contiguous(),
+                                        ks[perm].contiguous(), vq_[perm].contiguous(),
+                                        vs[perm].contiguous(), gs, 1 / math.sqrt(128))
+    assert torch.equal(out_p, out[perm])

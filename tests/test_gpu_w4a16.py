@@ -1,0 +1,84 @@
+"""GPU parity: W4A16 GEMV/GEMM and dequantise.
+
+Gate (written here): the fp32-output instantiation of the kernels is within
+2e-3 max-abs of the float64 oracle act @ (q * scale); the fp16 output equals
+round-to-nearest-even of that same fp32 accumulator, bit for bit. The fp16
+output is also reported against the oracle in fp16 ulps (<= 1 ulp + 2e-3),
+since |out| reaches ~10 at K=14336 where an fp16 half-ulp exceeds 2e-3.
+Weights follow the QuantizedLinear convention (fp32 W quantised,
+integration/w4a16_patch.py:78-84); dequantise is bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w4a16 as ow
+from tests.helpers import randn
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+LLAMA = [(4096, 4096), (4096, 14336), (14336, 4096)]
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+_CACHE = {}
+
+
+def _weights(K, N, gs, seed):
+    key = (K, N, gs, seed)
+    if key not in _CACHE:
+        W = randn((K, N), seed, scale=0.02)
+        q, s = ow.quantize_weights_int4_groupwise(W, gs)
+        _CACHE.clear()
+        _CACHE[key] = (q, s.astype(np.float16), ow.pack_int4_along_k(q))
+    return _CACHE[key]
+
+
+def _check(llmik, cuda, M, K, N, gs, seed):
+    q, s, packed = _weights(K, N, gs, seed)
+    act = randn((M, K), seed + 1).astype(np.float16)
+    a, w, sc = _dev(act, cuda), _dev(packed, cuda), _dev(s, cuda)
+    out32 = llmik.w4a16_gemm_f32out(a, w, sc, gs)
+    out16 = llmik.w4a16_gemm(a, w, sc, gs)
+    ref = ow.quantized_matmul_ref(act, q, s, gs, acc_dtype=np.float64)
+    o32 = out32.cpu().numpy()
+    assert np.abs(o32 - ref).max() <= TOL
+    assert np.array_equal(out16.cpu().numpy().view(np.uint16), o32.astype(np.float16).view(np.uint16))
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert (np.abs(out16.cpu().numpy().astype(np.float64) - ref) <= ulp + TOL).all()
+
+
+@pytest.mark.parametrize("K,N", LLAMA)
+@pytest.mark.parametrize("M", [1, 2, 16, 128])
+def test_llama_shapes(llmik, cuda, M, K, N):
+    _check(llmik, cuda, M, K, N, 128, seed=K + N)
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(1, 256, 64, 64), (3, 512, 100, 128), (1, 1024, 1000, 32),
+                                      (5, 128, 4, 128), (17, 768, 96, 256), (1, 8192, 36, 128),
+                                      (33, 256, 260, 64)])
+def test_odd_shapes(llmik, cuda, M, K, N, gs):
+    _check(llmik, cuda, M, K, N, gs, seed=M * 7 + K)
+
+
+def test_deterministic(llmik, cuda):
+    q, s, packed = _weights(4096, 4096, 128, 1)
+    a = _dev(randn((16, 4096), 2).astype(np.float16), cuda)
+    w, sc = _dev(packed, cuda), _dev(s, cuda)
+    first = llmik.w4a16_gemm(a, w, sc, 128)
+    for _ in range(3):
+        assert torch.equal(first, llmik.w4a16_gemm(a, w, sc, 128))
+
+
+@pytest.mark.parametrize("K,N,gs", [(4096, 4096, 128), (256, 100, 64), (512, 36, 128)])
+def test_dequantize_bit_exact(llmik, cuda, K, N, gs):
+    q, s, packed = _weights(K, N, gs, seed=K + 3)
+    out = llmik.w4a16_dequantize(_dev(packed, cuda), _dev(s, cuda), gs)
+    ref = ow.w4a16_dequantize_fp16(packed, s, gs)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
