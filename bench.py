@@ -84,11 +84,12 @@ def time_steps(steps_fns, warmup: int, reps: int):
             steps_fns[i % len(steps_fns)]()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    graph.replay()           # one untimed replay (page-in of the graph itself)
-    torch.cuda.synchronize()
-    start.record(stream)
-    graph.replay()
-    end.record(stream)
+    with torch.cuda.stream(stream):   # replay() launches on the current stream
+        graph.replay()                # one untimed replay (page-in of the graph itself)
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1000.0 / reps
     del graph

@@ -18,11 +18,12 @@
  *   8 codes along K (bits 4i..4i+3 = K position 8*k_pack + i).
  *
  * Workspace contract (attention and W4A16): query the size with the
- * matching *_workspace_size function. The start of the workspace holds
- * completion counters that must be zero before the first use; every
- * successful call leaves them zero again, so one zero-filled buffer can be
- * reused by consecutive calls on one stream. Calls that share a workspace
- * must not run concurrently.
+ * matching *_workspace_size function. The first LLMIK_WORKSPACE_COUNTER_BYTES
+ * bytes of every workspace hold completion counters: they must be zero
+ * before the first use, every successful call leaves them zero again, and
+ * no entry point writes anything else there. One zero-filled buffer can
+ * therefore be reused by consecutive calls of any of these entry points on
+ * one stream. Calls that share a workspace must not run concurrently.
  */
 #ifndef LLMIK_H
 #define LLMIK_H
@@ -44,6 +45,9 @@ typedef int llmik_status;
 #define LLMIK_ERR_UNSUPPORTED (-2)
 #define LLMIK_ERR_WORKSPACE (-3)
 #define LLMIK_ERR_ALIGNMENT (-4)
+
+/* Size of the zero-initialised counter region at the start of a workspace. */
+#define LLMIK_WORKSPACE_COUNTER_BYTES 16384
 
 /* Message for the last error raised on the calling thread ("" if none). */
 LLMIK_API const char* llmik_last_error(void);

@@ -5,23 +5,33 @@
 //   out[b,h,:] = softmax(scale * q[b,h] . K[b,h/G,0:S]^T) @ V[b,h/G,0:S]
 // with the cache addressed at stride kv_buf_len and read over [0, seqlen).
 //
-// Work decomposition
+// Work decomposition (both kernels below)
 //   * One workgroup owns one (batch, kv_head, head_chunk, split): the
 //     HPW <= 4 query heads that share a kv head are processed together, so
 //     every K/V byte of the split is read from HBM exactly once (the
 //     reference re-reads each kv head once per query head,
 //     kernels/attention/fused_attention_splitk.cu:84-90).
-//   * 256 threads = 16 DPP rows of 16 lanes. Lane c of a row owns the
-//     channels 8c..8c+7 of one token; row r walks the split's tokens
-//     r, r+16, r+32, ... four at a time, so each 64-token step of the
-//     workgroup reads one contiguous block of the cache.
-//   * Dot products are reduced inside a DPP row; each row keeps its own
-//     online-softmax state (m, l, o) in the log2 domain. Rows are merged
-//     through LDS at the end, then the split's un-normalised (o, m, l) is
-//     written to the workspace. The last workgroup to finish a
-//     (batch, kv_head, head_chunk) merges all splits and writes fp16 out,
-//     so a call is one kernel launch. The merge order is fixed (split 0..n),
-//     so results are deterministic.
+//   * Each workgroup keeps several online-softmax states (m, l, o) in the
+//     log2 domain, merges them through LDS, and writes the split's
+//     un-normalised (o, m, l) to the workspace. The last workgroup to finish
+//     a (batch, kv_head, head_chunk) merges all splits in split order and
+//     writes fp16 out, so a call is one launch and results are deterministic.
+//
+// Main kernel (decode_attention_mfma_kernel): each wave walks its own
+// contiguous token range in 32-token tiles on v_mfma_f32_16x16x32_f16:
+//   QK : A = q (16 rows, row m holds head m % HPW), B = 16 tokens' keys
+//        (lane = token, 8 consecutive channels per lane group) -> every lane
+//        gets the scores of its token for all heads; no lane reductions.
+//   PV : A = p (fp16, through a 256-byte per-wave LDS slot), B = values:
+//        lane (g, c) loads the channels 8c..8c+7 of tokens 8g..8g+7 (full
+//        cache rows per load instruction) and one v_perm_b32 per dword turns
+//        them into the B operand of MFMA j, which owns channels 8c + j.
+//   INT8/INT4 codes are converted to fp16 exactly in registers; the INT8
+//   per-token K scale multiplies the score, the per-token V scale folds into
+//   p, the INT4 per-channel K scale folds into q per group (q*s split into an
+//   fp16 hi + lo pair so the product keeps fp32 precision).
+// Fallback kernel (decode_attention_valu_kernel): fp32 VALU with 16-lane
+// DPP reductions; used for INT4 group sizes that are not multiples of 16.
 //
 // KV formats (packing is kernels/kv_cache/kv_compress.cuh:25-28 and
 // kernels/common/cuda_utils.cuh:85-119 of the reference):
@@ -38,10 +48,12 @@ namespace llmik {
 enum class KvFormat { F16, I8, I4 };
 
 constexpr int kAttnThreads = 256;
-constexpr int kRows = kAttnThreads / 16;   // 16 token rows per workgroup
-constexpr int kUnroll = 4;                 // tokens per row per step
-constexpr int kStepTokens = kRows * kUnroll;
 constexpr int kHeadDim = 128;
+constexpr int kChunkStep = 128;   // split sizes are multiples of this
+#ifndef LLMIK_ATTN_WGS_PER_CU
+#define LLMIK_ATTN_WGS_PER_CU 1
+#endif
+constexpr int kAttnWgsPerCu = LLMIK_ATTN_WGS_PER_CU;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -59,6 +71,526 @@ struct AttnParams {
     int n_splits, chunk, n_hchunks, gqa;
     float scale_log2;
 };
+
+// ---------------------------------------------------------------------------
+// Shared tail: merge NR partial states held in LDS, then either write the
+// output (single split) or publish the split and let the last one combine.
+// ---------------------------------------------------------------------------
+template <int NR, int HPW>
+__device__ __forceinline__ void finish_split(const AttnParams& p, const float (*s_o)[HPW][kHeadDim],
+                                             const float (*s_m)[HPW], const float (*s_l)[HPW],
+                                             uint32_t* s_last, int b, int kvh, int hchunk,
+                                             int split, int head0) {
+    const int tid = threadIdx.x;
+    constexpr int kOuts = HPW * kHeadDim;
+    constexpr int kPer = (kOuts + kAttnThreads - 1) / kAttnThreads;
+    const int slot_group = (b * p.n_kv_heads + kvh) * p.n_hchunks + hchunk;
+    const long slot = (long)slot_group * p.n_splits + split;
+    float wo[kPer], wm[kPer], wl[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = tid + i * kAttnThreads;
+        wo[i] = 0.0f;
+        wm[i] = -INFINITY;
+        wl[i] = 0.0f;
+        if (idx < kOuts) {
+            const int h = idx / kHeadDim, d = idx % kHeadDim;
+            float gm = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) gm = fmaxf(gm, s_m[r][h]);
+            float so = 0.0f, sl = 0.0f;
+            if (gm != -INFINITY) {
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    const float w = (s_m[r][h] == -INFINITY) ? 0.0f
+                                                              : __builtin_amdgcn_exp2f(s_m[r][h] - gm);
+                    so = fmaf(s_o[r][h][d], w, so);
+                    sl = fmaf(s_l[r][h], w, sl);
+                }
+            }
+            wo[i] = so;
+            wm[i] = gm;
+            wl[i] = sl;
+        }
+    }
+
+    if (p.n_splits == 1) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = tid + i * kAttnThreads;
+            if (idx < kOuts) {
+                const int h = idx / kHeadDim, d = idx % kHeadDim;
+                const float inv = (wl[i] > 0.0f) ? 1.0f / wl[i] : 0.0f;
+                p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(wo[i] * inv);
+            }
+        }
+        return;
+    }
+
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = tid + i * kAttnThreads;
+        if (idx < kOuts) {
+            const int h = idx / kHeadDim, d = idx % kHeadDim;
+            publish_store(&p.part_o[(slot * HPW + h) * kHeadDim + d], wo[i]);
+            if (d == 0) {
+                publish_store(&p.part_ml[(slot * HPW + h) * 2 + 0], wm[i]);
+                publish_store(&p.part_ml[(slot * HPW + h) * 2 + 1], wl[i]);
+            }
+        }
+    }
+    publish_wait();
+    __syncthreads();
+    if (tid == 0) *s_last = arrive_last(&p.counters[slot_group], (uint32_t)p.n_splits) ? 1u : 0u;
+    __syncthreads();
+    if (*s_last == 0u) return;
+
+    // Last split of this (batch, kv head, head chunk): combine all splits.
+    // The (m, l) pairs are gathered into LDS in one parallel step and the
+    // partial outputs are fetched in independent batches, so the combine
+    // costs a few memory round trips rather than one per split.
+    constexpr int kBatch = 8;
+    __shared__ float s_w[kMaxAttnSplits + kBatch][HPW];   // per-split m, then weight
+    __shared__ float s_ls[kMaxAttnSplits][HPW];           // per-split l
+    __shared__ float s_inv[HPW];
+    const long base = (long)slot_group * p.n_splits;
+    for (int idx = tid; idx < p.n_splits * HPW; idx += kAttnThreads) {
+        const int sp = idx / HPW, h = idx % HPW;
+        const float ms = publish_load(&p.part_ml[((base + sp) * HPW + h) * 2]);
+        const float ls = publish_load(&p.part_ml[((base + sp) * HPW + h) * 2 + 1]);
+        s_w[sp][h] = ms;
+        s_ls[sp][h] = ls;
+    }
+    __syncthreads();
+    if (tid < HPW) {
+        const int h = tid;
+        float gm = -INFINITY;
+        for (int sp = 0; sp < p.n_splits; ++sp) gm = fmaxf(gm, s_w[sp][h]);
+        float sl = 0.0f;
+        for (int sp = 0; sp < p.n_splits; ++sp) {
+            const float ms = s_w[sp][h];
+            const float w = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - gm);
+            s_w[sp][h] = w;
+            sl = fmaf(s_ls[sp][h], w, sl);
+        }
+        for (int sp = p.n_splits; sp < p.n_splits + kBatch; ++sp) s_w[sp][h] = 0.0f;
+        s_inv[h] = (sl > 0.0f) ? 1.0f / sl : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = tid + i * kAttnThreads;
+        if (idx < kOuts) {
+            const int h = idx / kHeadDim, d = idx % kHeadDim;
+            float so = 0.0f;
+            for (int sp0 = 0; sp0 < p.n_splits; sp0 += kBatch) {
+                float v[kBatch];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const int sp = min(sp0 + u, p.n_splits - 1);
+                    v[u] = publish_load(&p.part_o[((base + sp) * HPW + h) * kHeadDim + d]);
+                }
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) so = fmaf(v[u], s_w[sp0 + u][h], so);
+            }
+            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so * s_inv[h]);
+        }
+    }
+    if (tid == 0) p.counters[slot_group] = 0u;   // leave the counter zeroed for the next call
+}
+
+// ===========================================================================
+// MFMA kernel
+// ===========================================================================
+
+constexpr int kMfmaWaves = kAttnThreads / kWave;   // 4
+constexpr int kTile = 32;                          // tokens per wave step
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const f16x8 a, const f16x8 b, const f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f16x8 as_f16x8(const u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+
+__device__ __forceinline__ u32x4 make_u32x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    u32x4 r;
+    r[0] = a; r[1] = b; r[2] = c; r[3] = d;
+    return r;
+}
+
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Two biased int8 bytes (value + 128, in bytes 0 and 2 of x, bytes 1 and 3
+// zero) -> two exact fp16 values: 0x6400 | u is 1024 + u.
+__device__ __forceinline__ uint32_t u8pair_to_f16x2(uint32_t x) {
+    const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+    const f16x2 h = as_f16x2(x | 0x64006400u) - bias;
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Four int8 codes of one dword -> fp16 pairs (b0,b1), (b2,b3), exact.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    w ^= 0x80808080u;
+    lo = u8pair_to_f16x2(perm_b32(0u, w, 0x0C010C00u));
+    hi = u8pair_to_f16x2(perm_b32(0u, w, 0x0C030C02u));
+}
+
+// Eight int4 codes of one dword (already xor-biased by 8 per nibble) ->
+// fp16 pairs (n0,n4), (n1,n5), (n2,n6), (n3,n7), exact.
+__device__ __forceinline__ u32x4 i4x8b_to_f16(uint32_t w) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
+    const f16x2 a = as_f16x2((w & 0x000F000Fu) | 0x64006400u) - bias;
+    const f16x2 b = as_f16x2((w & 0x00F000F0u) | 0x64006400u) * sixteenth - bias16;
+    const f16x2 c = as_f16x2((w8 & 0x000F000Fu) | 0x64006400u) - bias;
+    const f16x2 d = as_f16x2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth - bias16;
+    return make_u32x4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                      __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d));
+}
+
+// Order of the channels inside an INT4 K operand: half e of the fp16 octet
+// made from one dword holds nibble i4_perm(e) (pairs (0,4), (1,5), (2,6), (3,7)).
+__host__ __device__ constexpr int i4_perm(int e) { return (e & 1) ? (e >> 1) + 4 : (e >> 1); }
+
+template <KvFormat F>
+struct MfmaTile;
+
+// ---- fp16 ------------------------------------------------------------------
+// QK operand of k-step ks for lane group g: channels 32*ks + 8*g + (0..7).
+template <>
+struct MfmaTile<KvFormat::F16> {
+    static constexpr float kPScale = 256.0f;   // p <= 1 -> fp16 p*256 has no subnormals above 2^-32
+    u32x4 k[2][4];
+    u32x4 v[8];
+    __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
+                                         int g, int c) {
+        const uint16_t* kp = static_cast<const uint16_t*>(p.k);
+        const uint16_t* vp = static_cast<const uint16_t*>(p.v);
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            const long row = row_base + min(t0 + 16 * blk + c, t_last);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) k[blk][ks] = load16(kp + row * kHeadDim + 32 * ks + 8 * g);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const long row = row_base + min(t0 + 8 * g + e, t_last);
+            v[e] = load16(vp + row * kHeadDim + 8 * c);
+        }
+    }
+    __device__ __forceinline__ f16x8 kop(int blk, int ks) const { return as_f16x8(k[blk][ks]); }
+    // B operand of PV MFMA j: (V[token 8g+2i][8c+j], V[token 8g+2i+1][8c+j]) per dword i.
+    __device__ __forceinline__ f16x8 vop(int j) const {
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        uint32_t d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = v[2 * i][j >> 1];
+            const uint32_t hi = v[2 * i + 1][j >> 1];
+            d[i] = perm_b32(hi, lo, sel);
+        }
+        return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
+    }
+};
+
+// ---- int8 ------------------------------------------------------------------
+// QK operand of k-step ks = 2u + h for lane group g: channels 64u + 16g + 8h + (0..7).
+template <>
+struct MfmaTile<KvFormat::I8> {
+    static constexpr float kPScale = 64.0f;    // p * v_scale * 64 <= 516 * 64 < 65504
+    u32x4 k[2][2];
+    u32x2 v[8];
+    uint16_t ks[2], vs[2];
+    __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
+                                         int g, int c) {
+        const int8_t* kp = static_cast<const int8_t*>(p.k);
+        const int8_t* vp = static_cast<const int8_t*>(p.v);
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            const long row = row_base + min(t0 + 16 * blk + c, t_last);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) k[blk][u] = load16(kp + row * kHeadDim + 64 * u + 16 * g);
+            ks[blk] = p.k_scale[row];
+            vs[blk] = p.v_scale[row];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const long row = row_base + min(t0 + 8 * g + e, t_last);
+            v[e] = load8(vp + row * kHeadDim + 8 * c);
+        }
+    }
+    __device__ __forceinline__ f16x8 kop(int blk, int ks_) const {
+        const u32x4 w = k[blk][ks_ >> 1];
+        const uint32_t w0 = w[(ks_ & 1) * 2], w1 = w[(ks_ & 1) * 2 + 1];
+        uint32_t a, b, c, d;
+        i8x4_to_f16(w0, a, b);
+        i8x4_to_f16(w1, c, d);
+        return as_f16x8(make_u32x4(a, b, c, d));
+    }
+    __device__ __forceinline__ f16x8 vop(int j) const {
+        const int byte = j & 3;
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
+        uint32_t d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = v[2 * i][j >> 2] ^ 0x80808080u;
+            const uint32_t hi = v[2 * i + 1][j >> 2] ^ 0x80808080u;
+            d[i] = u8pair_to_f16x2(perm_b32(hi, lo, sel));
+        }
+        return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
+    }
+};
+
+// ---- int4 ------------------------------------------------------------------
+// QK operand of k-step ks for lane group g: channels 32g + 8ks + i4_perm(e).
+template <>
+struct MfmaTile<KvFormat::I4> {
+    static constexpr float kPScale = 4.0f;     // p * v_scale * 4 <= 9358 * 4 < 65504
+    u32x4 k[2];
+    uint32_t v[8];
+    uint16_t vs[2];
+    __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
+                                         int g, int c) {
+        const int8_t* kp = static_cast<const int8_t*>(p.k);
+        const int8_t* vp = static_cast<const int8_t*>(p.v);
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            const long row = row_base + min(t0 + 16 * blk + c, t_last);
+            k[blk] = load16(kp + row * (kHeadDim / 2) + 16 * g);
+            vs[blk] = p.v_scale[row];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const long row = row_base + min(t0 + 8 * g + e, t_last);
+            v[e] = load4(vp + row * (kHeadDim / 2) + 4 * c);
+        }
+    }
+    __device__ __forceinline__ f16x8 kop(int blk, int ks_) const {
+        const uint32_t w = k[blk][ks_];
+        return as_f16x8(i4x8b_to_f16(w ^ 0x88888888u));
+    }
+    __device__ __forceinline__ f16x8 vop(int j) const {
+        const int byte = j >> 1;
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
+        const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
+        const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+        const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
+        uint32_t d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t x = perm_b32(v[2 * i + 1] ^ 0x88888888u, v[2 * i] ^ 0x88888888u, sel);
+            f16x2 h;
+            if (j & 1) h = as_f16x2((x & 0x00F000F0u) | 0x64006400u) * sixteenth - bias16;
+            else h = as_f16x2((x & 0x000F000Fu) | 0x64006400u) - bias;
+            d[i] = __builtin_bit_cast(uint32_t, h);
+        }
+        return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
+    }
+};
+
+template <KvFormat F, int HPW>
+__global__ __launch_bounds__(kAttnThreads) void decode_attention_mfma_kernel(AttnParams p) {
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y / p.n_hchunks;
+    const int hchunk = blockIdx.y % p.n_hchunks;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+
+    const int head0 = kvh * p.gqa + hchunk * HPW;
+    const long row_base = (long)(b * p.n_kv_heads + kvh) * p.kv_buf_len;
+    const uint16_t* qrow = p.q + ((long)b * p.n_heads + head0 + (c % HPW)) * kHeadDim;
+
+    // Q as the A operand (4 k-steps); for INT4 the hi/lo pair of q * k_scale.
+    f16x8 qa[4], qlo[4];
+    float qf[32];   // INT4 only: q in fp32 for this lane's 32 channels 32g..32g+31
+    if constexpr (F == KvFormat::F16) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qa[ks] = as_f16x8(load16(qrow + 32 * ks + 8 * g));
+    } else if constexpr (F == KvFormat::I8) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            qa[ks] = as_f16x8(load16(qrow + 64 * (ks >> 1) + 16 * g + 8 * (ks & 1)));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float t[8];
+            f16x8_to_f32(load16(qrow + 32 * g + 8 * i), t);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[8 * i + e] = t[e];
+        }
+    }
+
+    f32x4 o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
+    }
+
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[kMfmaWaves][4][kTile];
+
+    const int t_begin = split * p.chunk;
+    const int t_end = min(t_begin + p.chunk, p.seqlen);
+    const int per_wave = p.chunk / kMfmaWaves;   // multiple of kTile
+    const int w0 = min(t_begin + wave * per_wave, t_end);
+    const int w1 = min(w0 + per_wave, t_end);
+    int cur_group = -1;
+
+    auto step = [&](const MfmaTile<F>& tile, const int t0) {
+
+        // ---- scores for the tile's two 16-token blocks ----
+        float s[2][4];
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            if constexpr (F == KvFormat::I4) {
+                const int grp = (t0 + 16 * blk) / p.group_size;
+                if (grp != cur_group) {
+                    cur_group = grp;
+                    const uint16_t* ksrow = p.k_scale +
+                        ((long)(b * p.n_kv_heads + kvh) * p.n_groups + grp) * kHeadDim + 32 * g;
+                    float sc[32];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float t[8];
+                        f16x8_to_f32(load16(ksrow + 8 * i), t);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) sc[8 * i + e] = t[e];
+                    }
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        f16x8 hi, lo;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int ch = 8 * ks + i4_perm(e);
+                            const float x = qf[ch] * sc[ch];
+                            const f16 xh = (f16)x;
+                            hi[e] = xh;
+                            lo[e] = (f16)(x - (float)xh);
+                        }
+                        qa[ks] = hi;
+                        qlo[ks] = lo;
+                    }
+                }
+            }
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const f16x8 kb = tile.kop(blk, ks);
+                acc = mfma16x16x32(qa[ks], kb, acc);
+                if constexpr (F == KvFormat::I4) acc = mfma16x16x32(qlo[ks], kb, acc);
+            }
+            const bool valid = (t0 + 16 * blk + c) < w1;
+            float sc = p.scale_log2;
+            if constexpr (F == KvFormat::I8) sc *= h2f(tile.ks[blk]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[blk][i] = valid ? acc[i] * sc : -INFINITY;
+        }
+
+        // ---- online softmax over the 32 tokens (identical in all 4 lane groups) ----
+        float pr[2][4];
+        bool rescale = false;
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float tmax = row16_max(fmaxf(s[0][i], s[1][i]));
+            const float mn = fmaxf(m[i], tmax);
+            const float msafe = (mn == -INFINITY) ? 0.0f : mn;
+            alpha[i] = __builtin_amdgcn_exp2f(m[i] - msafe);
+            rescale |= (mn != m[i]);
+            m[i] = mn;
+            pr[0][i] = __builtin_amdgcn_exp2f(s[0][i] - msafe);
+            pr[1][i] = __builtin_amdgcn_exp2f(s[1][i] - msafe);
+            l[i] = fmaf(l[i], alpha[i], pr[0][i] + pr[1][i]);
+        }
+        if (rescale) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[j][i] *= alpha[i];
+        }
+
+        // ---- p -> LDS (lane group g writes head g) -> A operand ----
+        if (g < HPW) {
+            float f0 = MfmaTile<F>::kPScale, f1 = MfmaTile<F>::kPScale;
+            if constexpr (F != KvFormat::F16) {
+                f0 *= h2f(tile.vs[0]);
+                f1 *= h2f(tile.vs[1]);
+            }
+            s_p[wave][g][c] = f2h_bits(pr[0][g] * f0);
+            s_p[wave][g][16 + c] = f2h_bits(pr[1][g] * f1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const f16x8 pa = as_f16x8(load16(&s_p[wave][c % HPW][8 * g]));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+
+        // ---- O += P V ----
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(j), o[j]);
+    };
+
+    // Two tile buffers: the next tile's loads are in flight while the
+    // current tile is processed.
+    MfmaTile<F> ta, tb;
+    int t0 = w0;
+    if (t0 < w1) ta.load(p, row_base, t0, w1 - 1, g, c);
+    while (t0 < w1) {
+        const int t1 = t0 + kTile;
+        if (t1 < w1) tb.load(p, row_base, t1, w1 - 1, g, c);
+        step(ta, t0);
+        if (t1 >= w1) break;
+        const int t2 = t1 + kTile;
+        if (t2 < w1) ta.load(p, row_base, t2, w1 - 1, g, c);
+        step(tb, t1);
+        t0 = t2;
+    }
+
+    // ---- merge the 4 wave states through LDS ----
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l[i] = row16_sum(l[i]);
+
+    __shared__ float s_o[kMfmaWaves][HPW][kHeadDim];
+    __shared__ float s_m[kMfmaWaves][HPW];
+    __shared__ float s_l[kMfmaWaves][HPW];
+    __shared__ uint32_t s_last;
+    constexpr float kInvP = 1.0f / MfmaTile<F>::kPScale;
+    if (g == 0) {
+#pragma unroll
+        for (int i = 0; i < HPW; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s_o[wave][i][8 * c + j] = o[j][i] * kInvP;
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < HPW; ++i) {
+            s_m[wave][i] = m[i];
+            s_l[wave][i] = l[i];
+        }
+    }
+    __syncthreads();
+    finish_split<kMfmaWaves, HPW>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
+}
+
+// ===========================================================================
+// VALU fallback kernel
+// ===========================================================================
+
+constexpr int kRows = kAttnThreads / 16;   // 16 token rows per workgroup
+constexpr int kUnroll = 4;                 // tokens per row per step
+constexpr int kStepTokens = kRows * kUnroll;
 
 template <KvFormat F>
 struct KvRow;
@@ -111,8 +643,11 @@ struct KvRow<KvFormat::I4> {
     __device__ __forceinline__ float v_token_scale() const { return h2f(vs); }
 };
 
+// 16 rows of 16 lanes: lane c of a row owns channels 8c..8c+7 of one token;
+// row r walks the split's tokens r, r+16, ... four at a time; dot products
+// are reduced inside the DPP row and each row keeps its own softmax state.
 template <KvFormat F, int HPW>
-__global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(kAttnThreads) void decode_attention_valu_kernel(AttnParams p) {
     const int split = blockIdx.x;
     const int kvh = blockIdx.y / p.n_hchunks;
     const int hchunk = blockIdx.y % p.n_hchunks;
@@ -146,7 +681,6 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(AttnPara
     const int t_begin = split * p.chunk;
     const int t_end = min(t_begin + p.chunk, p.seqlen);
 
-    // INT4 K scales: per-channel, constant over a group of tokens.
     int cur_group = -1;
     float kscale[8];
 #pragma unroll
@@ -170,11 +704,11 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(AttnPara
             float kf[8];
             kv[u].k_f32(kf);
             if constexpr (F == KvFormat::I4) {
-                const int g = min(tok[u], t_end - 1) / p.group_size;
-                if (g != cur_group) {
-                    cur_group = g;
+                const int gi = min(tok[u], t_end - 1) / p.group_size;
+                if (gi != cur_group) {
+                    cur_group = gi;
                     float tmp[8];
-                    f16x8_to_f32(load16(ks_base + (long)g * kHeadDim), tmp);
+                    f16x8_to_f32(load16(ks_base + (long)gi * kHeadDim), tmp);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) kscale[e] = tmp[e];
                 }
@@ -222,7 +756,6 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(AttnPara
         }
     }
 
-    // ---- merge the 16 row states of this workgroup through LDS ----
     __shared__ float s_o[kRows][HPW][kHeadDim];
     __shared__ float s_m[kRows][HPW];
     __shared__ float s_l[kRows][HPW];
@@ -237,101 +770,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(AttnPara
         }
     }
     __syncthreads();
-
-    constexpr int kOuts = HPW * kHeadDim;
-    const int slot_group = (b * p.n_kv_heads + kvh) * p.n_hchunks + hchunk;
-    const long slot = (long)slot_group * p.n_splits + split;
-    float wo[(kOuts + kAttnThreads - 1) / kAttnThreads];
-    float wm[(kOuts + kAttnThreads - 1) / kAttnThreads];
-    float wl[(kOuts + kAttnThreads - 1) / kAttnThreads];
-#pragma unroll
-    for (int i = 0; i < (kOuts + kAttnThreads - 1) / kAttnThreads; ++i) {
-        const int idx = tid + i * kAttnThreads;
-        wo[i] = 0.0f;
-        wm[i] = -INFINITY;
-        wl[i] = 0.0f;
-        if (idx < kOuts) {
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-            float gm = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) gm = fmaxf(gm, s_m[r][h]);
-            float so = 0.0f, sl = 0.0f;
-            if (gm != -INFINITY) {
-#pragma unroll
-                for (int r = 0; r < kRows; ++r) {
-                    const float w = (s_m[r][h] == -INFINITY)
-                                        ? 0.0f
-                                        : __builtin_amdgcn_exp2f(s_m[r][h] - gm);
-                    so = fmaf(s_o[r][h][d], w, so);
-                    sl = fmaf(s_l[r][h], w, sl);
-                }
-            }
-            wo[i] = so;
-            wm[i] = gm;
-            wl[i] = sl;
-        }
-    }
-
-    if (p.n_splits == 1) {
-#pragma unroll
-        for (int i = 0; i < (kOuts + kAttnThreads - 1) / kAttnThreads; ++i) {
-            const int idx = tid + i * kAttnThreads;
-            if (idx < kOuts) {
-                const int h = idx / kHeadDim, d = idx % kHeadDim;
-                const float inv = (wl[i] > 0.0f) ? 1.0f / wl[i] : 0.0f;
-                p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(wo[i] * inv);
-            }
-        }
-        return;
-    }
-
-    // ---- publish this split's partial; the last split to land combines ----
-#pragma unroll
-    for (int i = 0; i < (kOuts + kAttnThreads - 1) / kAttnThreads; ++i) {
-        const int idx = tid + i * kAttnThreads;
-        if (idx < kOuts) {
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-            p.part_o[(slot * HPW + h) * kHeadDim + d] = wo[i];
-            if (d == 0) {
-                p.part_ml[(slot * HPW + h) * 2 + 0] = wm[i];
-                p.part_ml[(slot * HPW + h) * 2 + 1] = wl[i];
-            }
-        }
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&p.counters[slot_group], 1u);
-        s_last = (prev == (uint32_t)(p.n_splits - 1)) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (s_last == 0u) return;
-    __threadfence();
-
-#pragma unroll
-    for (int i = 0; i < (kOuts + kAttnThreads - 1) / kAttnThreads; ++i) {
-        const int idx = tid + i * kAttnThreads;
-        if (idx < kOuts) {
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-            const long base = (long)slot_group * p.n_splits;
-            float gm = -INFINITY;
-            for (int sp = 0; sp < p.n_splits; ++sp)
-                gm = fmaxf(gm, __builtin_nontemporal_load(&p.part_ml[((base + sp) * HPW + h) * 2]));
-            float so = 0.0f, sl = 0.0f;
-            if (gm != -INFINITY) {
-                for (int sp = 0; sp < p.n_splits; ++sp) {
-                    const float ms = __builtin_nontemporal_load(&p.part_ml[((base + sp) * HPW + h) * 2]);
-                    if (ms == -INFINITY) continue;
-                    const float w = __builtin_amdgcn_exp2f(ms - gm);
-                    so = fmaf(__builtin_nontemporal_load(&p.part_o[((base + sp) * HPW + h) * kHeadDim + d]), w, so);
-                    sl = fmaf(__builtin_nontemporal_load(&p.part_ml[((base + sp) * HPW + h) * 2 + 1]), w, sl);
-                }
-            }
-            const float inv = (sl > 0.0f) ? 1.0f / sl : 0.0f;
-            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so * inv);
-        }
-    }
-    if (tid == 0) p.counters[slot_group] = 0u;   // leave the counter zeroed for the next call
+    finish_split<kRows, HPW>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
 }
 
 // ---------------------------------------------------------------------------
@@ -355,28 +794,39 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
     pl.n_hchunks = gqa / pl.hpw;
     const long base_wgs = (long)batch * n_kv_heads * pl.n_hchunks;
     const int cus = device_cu_count();
-    // Aim for ~4 resident workgroups per CU, with at least one 64-token step
-    // per split so every split does real work.
-    const long target = 4L * cus;
+    // Aim for kAttnWgsPerCu workgroups per CU; every split gets at least
+    // one 128-token step (32 tokens per wave).
+    const long target = (long)kAttnWgsPerCu * cus;
     long want = (target + base_wgs - 1) / base_wgs;
-    const long max_useful = (seqlen + kStepTokens - 1) / kStepTokens;
+    const long max_useful = (seqlen + kChunkStep - 1) / kChunkStep;
     if (want > max_useful) want = max_useful;
     if (want > kMaxAttnSplits) want = kMaxAttnSplits;
+    if (base_wgs > kMaxCounters) want = 1;   // enough workgroups without splitting
     if (want < 1) want = 1;
     int chunk = (int)((seqlen + want - 1) / want);
-    chunk = ((chunk + kStepTokens - 1) / kStepTokens) * kStepTokens;
-    if (chunk < kStepTokens) chunk = kStepTokens;
+    chunk = ((chunk + kChunkStep - 1) / kChunkStep) * kChunkStep;
+    if (chunk < kChunkStep) chunk = kChunkStep;
     pl.chunk = chunk;
     pl.n_splits = seqlen > 0 ? (seqlen + chunk - 1) / chunk : 1;
     pl.n_slot_groups = base_wgs;
-    const size_t counters = align_up((size_t)base_wgs * sizeof(uint32_t), 256);
     const size_t slots = (size_t)base_wgs * pl.n_splits * pl.hpw;
     const size_t ml = align_up(slots * 2 * sizeof(float), 256);
     const size_t po = align_up(slots * kHeadDim * sizeof(float), 256);
-    pl.workspace_bytes = (pl.n_splits > 1) ? counters + ml + po : 0;
-    pl.off_ml = counters;
-    pl.off_o = counters + ml;
+    pl.workspace_bytes = (pl.n_splits > 1) ? kCounterBytes + ml + po : 0;
+    pl.off_ml = kCounterBytes;
+    pl.off_o = kCounterBytes + ml;
     return pl;
+}
+
+template <KvFormat F, int HPW>
+static void launch_kernel(const AttnParams& p, dim3 grid, bool mfma, hipStream_t stream) {
+    if (mfma) {
+        hipLaunchKernelGGL((decode_attention_mfma_kernel<F, HPW>), grid, dim3(kAttnThreads), 0,
+                           stream, p);
+    } else {
+        hipLaunchKernelGGL((decode_attention_valu_kernel<F, HPW>), grid, dim3(kAttnThreads), 0,
+                           stream, p);
+    }
 }
 
 template <KvFormat F>
@@ -408,12 +858,13 @@ static int launch_attention(const AttnLaunch& a, hipStream_t stream) {
     p.gqa = a.n_heads / a.n_kv_heads;
     p.scale_log2 = a.softmax_scale * kLog2e;
 
+    // The MFMA path keeps 16-token blocks inside one INT4 K-scale group.
+    const bool mfma = (F != KvFormat::I4) || (p.group_size % 16 == 0);
     dim3 grid(pl.n_splits, a.n_kv_heads * pl.n_hchunks, a.batch);
-    dim3 block(kAttnThreads);
     switch (pl.hpw) {
-        case 4: hipLaunchKernelGGL((decode_attention_kernel<F, 4>), grid, block, 0, stream, p); break;
-        case 2: hipLaunchKernelGGL((decode_attention_kernel<F, 2>), grid, block, 0, stream, p); break;
-        default: hipLaunchKernelGGL((decode_attention_kernel<F, 1>), grid, block, 0, stream, p); break;
+        case 4: launch_kernel<F, 4>(p, grid, mfma, stream); break;
+        case 2: launch_kernel<F, 2>(p, grid, mfma, stream); break;
+        default: launch_kernel<F, 1>(p, grid, mfma, stream); break;
     }
     return check_launch();
 }

@@ -60,11 +60,17 @@ __device__ __forceinline__ uint16_t f2h_bits(float x) {
     return __builtin_bit_cast(uint16_t, (f16)x);  // v_cvt_f16_f32, RNE
 }
 
+// NOTE: __builtin_bit_cast applied directly to an ext-vector element
+// (`__builtin_bit_cast(f16x2, v[i])`) is miscompiled by this hipcc (every
+// element reads as element 0). Always copy the element to a scalar first.
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t w) { return __builtin_bit_cast(f16x2, w); }
+
 // Unpack 8 fp16 stored in a 16-byte vector into fp32.
 __device__ __forceinline__ void f16x8_to_f32(const u32x4 raw, float out[8]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const f16x2 h = __builtin_bit_cast(f16x2, raw[i]);
+        const uint32_t w = raw[i];
+        const f16x2 h = as_f16x2(w);
         out[2 * i] = (float)h[0];
         out[2 * i + 1] = (float)h[1];
     }
@@ -100,6 +106,29 @@ __device__ __forceinline__ u32x2 load8(const void* p) {
 }
 __device__ __forceinline__ uint32_t load4(const void* p) {
     return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// ---- cross-workgroup hand-off -------------------------------------------------
+// Split partials travel between workgroups that may sit on different XCDs,
+// whose L2 caches are not coherent with each other. An agent-scope relaxed
+// atomic store/load is a plain `global_store/global_load ... sc1`, coherent
+// across the device without the whole-L2 write-back / invalidate that an
+// agent-scope fence (__threadfence) costs per workgroup. Every producing
+// wave calls publish_wait() (s_waitcnt 0: its stores are complete) before
+// the workgroup barrier that precedes the completion-counter increment; the
+// consumer reads the partials with publish_load after it has seen the final
+// count. (A plain __syncthreads does not wait for outstanding global stores
+// on gfx950.)
+__device__ __forceinline__ void publish_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float publish_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_wait() { __builtin_amdgcn_s_waitcnt(0); }
+// Returns true in exactly one workgroup: the last of `n` to arrive.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t n) {
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
 }
 
 // ---- exact symmetric quantisation step ------------------------------------

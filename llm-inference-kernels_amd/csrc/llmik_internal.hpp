@@ -11,6 +11,11 @@
 namespace llmik {
 
 constexpr int kMaxAttnSplits = 256;
+// Completion counters live in a fixed region at the start of every
+// workspace; split partials always start after it, so counters of one call
+// never alias partials of another.
+constexpr size_t kCounterBytes = LLMIK_WORKSPACE_COUNTER_BYTES;
+constexpr long kMaxCounters = (long)(kCounterBytes / sizeof(uint32_t));
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 

@@ -49,22 +49,39 @@ __device__ __forceinline__ void i4x8_to_f16_pairs(uint32_t w, f16x2 out[4]) {
     const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
     const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
     const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
-    out[0] = __builtin_bit_cast(f16x2, a) - bias;
-    out[1] = __builtin_bit_cast(f16x2, b) * sixteenth - bias16;
-    out[2] = __builtin_bit_cast(f16x2, c) - bias;
-    out[3] = __builtin_bit_cast(f16x2, d) * sixteenth - bias16;
+    out[0] = as_f16x2(a) - bias;
+    out[1] = as_f16x2(b) * sixteenth - bias16;
+    out[2] = as_f16x2(c) - bias;
+    out[3] = as_f16x2(d) * sixteenth - bias16;
 }
 
 // Activation pairs matching i4x8_to_f16_pairs: (a0,a4), (a1,a5), (a2,a6), (a3,a7).
 __device__ __forceinline__ void act_pairs(const u32x4 a, f16x2 out[4]) {
-    const f16x2 lo0 = __builtin_bit_cast(f16x2, a[0]);   // a0 a1
-    const f16x2 lo1 = __builtin_bit_cast(f16x2, a[1]);   // a2 a3
-    const f16x2 hi0 = __builtin_bit_cast(f16x2, a[2]);   // a4 a5
-    const f16x2 hi1 = __builtin_bit_cast(f16x2, a[3]);   // a6 a7
+    const uint32_t w0 = a[0], w1 = a[1], w2 = a[2], w3 = a[3];
+    const f16x2 lo0 = as_f16x2(w0);   // a0 a1
+    const f16x2 lo1 = as_f16x2(w1);   // a2 a3
+    const f16x2 hi0 = as_f16x2(w2);   // a4 a5
+    const f16x2 hi1 = as_f16x2(w3);   // a6 a7
     out[0] = f16x2{lo0[0], hi0[0]};
     out[1] = f16x2{lo0[1], hi0[1]};
     out[2] = f16x2{lo1[0], hi1[0]};
     out[3] = f16x2{lo1[1], hi1[1]};
+}
+
+// Sum of n split partials p[0], p[stride], ... in split order. The loads are
+// issued in independent batches so the reduction costs a few memory round
+// trips instead of one per split.
+__device__ __forceinline__ float sum_splits(const float* p, long stride, int n) {
+    constexpr int kBatch = 8;
+    float v = 0.0f;
+    for (int s0 = 0; s0 < n; s0 += kBatch) {
+        float x[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) x[u] = publish_load(p + (long)min(s0 + u, n - 1) * stride);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v += (s0 + u < n) ? x[u] : 0.0f;
+    }
+    return v;
 }
 
 // Store the workgroup's column-tile result, or publish it as a split partial
@@ -172,25 +189,18 @@ __global__ __launch_bounds__(kGemmThreads) void w4a16_gemv_kernel(GemmParams p) 
 #pragma unroll
     for (int i = 0; i < (64 * COLS + kGemmThreads - 1) / kGemmThreads; ++i) {
         const int col = threadIdx.x + i * kGemmThreads;
-        if (col < tile_n && nbase + col < p.N) p.part[(long)split * p.N + nbase + col] = tot[i];
+        if (col < tile_n && nbase + col < p.N) publish_store(&p.part[(long)split * p.N + nbase + col], tot[i]);
     }
-    __threadfence();
+    publish_wait();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&p.counters[tile], 1u);
-        s_last = (prev == (uint32_t)(p.splits - 1)) ? 1u : 0u;
-    }
+    if (threadIdx.x == 0) s_last = arrive_last(&p.counters[tile], (uint32_t)p.splits) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
-    __threadfence();
 #pragma unroll
     for (int i = 0; i < (64 * COLS + kGemmThreads - 1) / kGemmThreads; ++i) {
         const int col = threadIdx.x + i * kGemmThreads;
-        if (col < tile_n && nbase + col < p.N) {
-            float v = 0.0f;
-            for (int sp = 0; sp < p.splits; ++sp) v += p.part[(long)sp * p.N + nbase + col];
-            store_out(p, 0, nbase + col, v);
-        }
+        if (col < tile_n && nbase + col < p.N)
+            store_out(p, 0, nbase + col, sum_splits(p.part + nbase + col, (long)p.N, p.splits));
     }
     if (threadIdx.x == 0) p.counters[tile] = 0u;
 }
@@ -295,27 +305,21 @@ __global__ __launch_bounds__(kGemmThreads) void w4a16_gemm_tiled_kernel(GemmPara
         const int idx = threadIdx.x + i * kGemmThreads;
         const int m = idx / tile_n, col = idx % tile_n;
         if (idx < outs && m < mrows && nbase + col < p.N)
-            p.part[((long)split * p.M + m0 + m) * p.N + nbase + col] = tot[i];
+            publish_store(&p.part[((long)split * p.M + m0 + m) * p.N + nbase + col], tot[i]);
     }
-    __threadfence();
+    publish_wait();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&p.counters[counter], 1u);
-        s_last = (prev == (uint32_t)(p.splits - 1)) ? 1u : 0u;
-    }
+    if (threadIdx.x == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
-    __threadfence();
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const int idx = threadIdx.x + i * kGemmThreads;
         const int m = idx / tile_n, col = idx % tile_n;
-        if (idx < outs && m < mrows && nbase + col < p.N) {
-            float v = 0.0f;
-            for (int sp = 0; sp < p.splits; ++sp)
-                v += p.part[((long)sp * p.M + m0 + m) * p.N + nbase + col];
-            store_out(p, m0 + m, nbase + col, v);
-        }
+        if (idx < outs && m < mrows && nbase + col < p.N)
+            store_out(p, m0 + m, nbase + col,
+                      sum_splits(p.part + (long)(m0 + m) * p.N + nbase + col, (long)p.M * p.N,
+                                 p.splits));
     }
     if (threadIdx.x == 0) p.counters[counter] = 0u;
 }
@@ -381,15 +385,15 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     long want = (2L * cus + base - 1) / base;
     const long max_splits = (kp_total + 4 * kGemmWaves - 1) / (4 * kGemmWaves);
     if (want > max_splits) want = max_splits;
+    if (base > kMaxCounters) want = 1;   // enough workgroups without splitting
     if (want < 1) want = 1;
     int kps = (int)((kp_total + want - 1) / want);
     kps = (kps + kGemmWaves - 1) / kGemmWaves * kGemmWaves;
     pl.kp_per_split = kps;
     pl.splits = (kp_total + kps - 1) / kps;
-    const size_t counters = align_up((size_t)base * sizeof(uint32_t), 256);
     const size_t part = align_up((size_t)pl.splits * M * N * sizeof(float), 256);
-    pl.off_part = counters;
-    pl.workspace_bytes = (pl.splits > 1) ? counters + part : 0;
+    pl.off_part = kCounterBytes;
+    pl.workspace_bytes = (pl.splits > 1) ? kCounterBytes + part : 0;
     return pl;
 }
 

@@ -1,0 +1,85 @@
+"""GPU: the shared per-stream workspace. Calls of different ops and plans
+interleave on one stream; stale split partials left past the counter region
+must never be read as completion counters (regression: a W4A16 call with
+256 column tiles once read an earlier attention call's partials as
+counters)."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import w4a16 as ow
+from tests.helpers import randn
+
+pytestmark = pytest.mark.gpu
+
+COUNTER_BYTES = 16384
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _poison_workspaces(llmik):
+    torch.cuda.synchronize()
+    for ws in llmik._WORKSPACES.values():
+        ws[COUNTER_BYTES:].fill_(0xA5)
+        assert int(ws[:COUNTER_BYTES].count_nonzero()) == 0   # counters were left zeroed
+
+
+def _attn_case(llmik, cuda, B, S, seed):
+    q = randn((B, 32, 128), seed).astype(np.float16)
+    k = randn((B, 8, S, 128), seed + 1).astype(np.float16)
+    v = randn((B, 8, S, 128), seed + 2).astype(np.float16)
+    out = llmik.decode_attention(_dev(q, cuda), _dev(k, cuda), _dev(v, cuda), 1 / math.sqrt(128))
+    ref = oa.decode_attention(q, k, v, 1 / math.sqrt(128))
+    assert float(np.abs(out.float().cpu().numpy() - ref).max()) <= 2e-3
+
+
+def _gemm_case(llmik, cuda, M, K, N, seed):
+    W = randn((K, N), seed, scale=0.02)
+    q, s = ow.quantize_weights_int4_groupwise(W, 128)
+    s = s.astype(np.float16)
+    act = randn((M, K), seed + 1).astype(np.float16)
+    out = llmik.w4a16_gemm_f32out(_dev(act, cuda), _dev(ow.pack_int4_along_k(q), cuda),
+                                  _dev(s, cuda), 128)
+    ref = ow.quantized_matmul_ref(act, q, s, 128, acc_dtype=np.float64)
+    assert float(np.abs(out.cpu().numpy() - ref).max()) <= 2e-3
+
+
+def test_interleaved_ops_with_poisoned_partials(llmik, cuda):
+    _attn_case(llmik, cuda, 2, 16384, 1)      # many splits, large partials
+    _poison_workspaces(llmik)
+    _gemm_case(llmik, cuda, 128, 4096, 4096, 2)   # 256 column x row tiles, split K
+    _poison_workspaces(llmik)
+    _gemm_case(llmik, cuda, 1, 4096, 4096, 3)
+    _poison_workspaces(llmik)
+    _attn_case(llmik, cuda, 8, 4096, 4)
+    _poison_workspaces(llmik)
+    _gemm_case(llmik, cuda, 16, 14336, 4096, 5)
+    _poison_workspaces(llmik)
+    _attn_case(llmik, cuda, 1, 100, 6)
+
+
+@pytest.mark.parametrize("B,S", [(1, 16384), (2, 4096), (8, 4096)])
+def test_split_handoff_is_deterministic(llmik, cuda, B, S):
+    """Many splits per (batch, kv head): 40 repeated calls must agree bit for
+    bit with the first (a stale or torn partial would show up as a change)."""
+    gen = torch.Generator(device=cuda).manual_seed(B * S)
+    q = torch.randn((B, 32, 128), generator=gen, device=cuda, dtype=torch.float16)
+    k = torch.randn((B, 8, S, 128), generator=gen, device=cuda, dtype=torch.float16)
+    v = torch.randn((B, 8, S, 128), generator=gen, device=cuda, dtype=torch.float16)
+    first = llmik.decode_attention(q, k, v, 0.0883883)
+    outs = [llmik.decode_attention(q, k, v, 0.0883883) for _ in range(40)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(first, o) for o in outs)
+    act = torch.randn((1, 4096), generator=gen, device=cuda, dtype=torch.float16)
+    w = torch.randint(-2 ** 31, 2 ** 31 - 1, (512, 4096), generator=gen, device=cuda,
+                      dtype=torch.int32)
+    sc = (torch.rand((32, 4096), generator=gen, device=cuda) * 0.01).half()
+    g0 = llmik.w4a16_gemm_f32out(act, w, sc, 128)
+    assert all(torch.equal(g0, llmik.w4a16_gemm_f32out(act, w, sc, 128)) for _ in range(40))
