@@ -146,54 +146,45 @@ __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*
     if (*s_last == 0u) return;
 
     // Last split of this (batch, kv head, head chunk): combine all splits.
-    // The (m, l) pairs are gathered into LDS in one parallel step and the
-    // partial outputs are fetched in independent batches, so the combine
-    // costs a few memory round trips rather than one per split.
-    constexpr int kBatch = 8;
-    __shared__ float s_w[kMaxAttnSplits + kBatch][HPW];   // per-split m, then weight
-    __shared__ float s_ls[kMaxAttnSplits][HPW];           // per-split l
-    __shared__ float s_inv[HPW];
+    // Each thread issues the (m, l) and partial-output loads of a batch of
+    // splits together, so a combine of up to kBatch splits costs one memory
+    // round trip; rescaling to a common maximum is done in registers.
+    constexpr int kBatch = 16;
     const long base = (long)slot_group * p.n_splits;
-    for (int idx = tid; idx < p.n_splits * HPW; idx += kAttnThreads) {
-        const int sp = idx / HPW, h = idx % HPW;
-        const float ms = publish_load(&p.part_ml[((base + sp) * HPW + h) * 2]);
-        const float ls = publish_load(&p.part_ml[((base + sp) * HPW + h) * 2 + 1]);
-        s_w[sp][h] = ms;
-        s_ls[sp][h] = ls;
-    }
-    __syncthreads();
-    if (tid < HPW) {
-        const int h = tid;
-        float gm = -INFINITY;
-        for (int sp = 0; sp < p.n_splits; ++sp) gm = fmaxf(gm, s_w[sp][h]);
-        float sl = 0.0f;
-        for (int sp = 0; sp < p.n_splits; ++sp) {
-            const float ms = s_w[sp][h];
-            const float w = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - gm);
-            s_w[sp][h] = w;
-            sl = fmaf(s_ls[sp][h], w, sl);
-        }
-        for (int sp = p.n_splits; sp < p.n_splits + kBatch; ++sp) s_w[sp][h] = 0.0f;
-        s_inv[h] = (sl > 0.0f) ? 1.0f / sl : 0.0f;
-    }
-    __syncthreads();
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const int idx = tid + i * kAttnThreads;
         if (idx < kOuts) {
             const int h = idx / kHeadDim, d = idx % kHeadDim;
-            float so = 0.0f;
+            float gm = -INFINITY, so = 0.0f, sl = 0.0f;
             for (int sp0 = 0; sp0 < p.n_splits; sp0 += kBatch) {
-                float v[kBatch];
+                float mv[kBatch], lv[kBatch], ov[kBatch];
 #pragma unroll
                 for (int u = 0; u < kBatch; ++u) {
-                    const int sp = min(sp0 + u, p.n_splits - 1);
-                    v[u] = publish_load(&p.part_o[((base + sp) * HPW + h) * kHeadDim + d]);
+                    const long sl_idx = (base + min(sp0 + u, p.n_splits - 1)) * HPW + h;
+                    mv[u] = publish_load(&p.part_ml[sl_idx * 2]);
+                    lv[u] = publish_load(&p.part_ml[sl_idx * 2 + 1]);
+                    ov[u] = publish_load(&p.part_o[sl_idx * kHeadDim + d]);
                 }
+                float bm = gm;
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) so = fmaf(v[u], s_w[sp0 + u][h], so);
+                for (int u = 0; u < kBatch; ++u)
+                    if (sp0 + u < p.n_splits) bm = fmaxf(bm, mv[u]);
+                if (bm == -INFINITY) continue;
+                const float r = (gm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(gm - bm);
+                so *= r;
+                sl *= r;
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const float w = (sp0 + u < p.n_splits && mv[u] != -INFINITY)
+                                        ? __builtin_amdgcn_exp2f(mv[u] - bm) : 0.0f;
+                    so = fmaf(ov[u], w, so);
+                    sl = fmaf(lv[u], w, sl);
+                }
+                gm = bm;
             }
-            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so * s_inv[h]);
+            const float inv = (sl > 0.0f) ? 1.0f / sl : 0.0f;
+            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so * inv);
         }
     }
     if (tid == 0) p.counters[slot_group] = 0u;   // leave the counter zeroed for the next call
@@ -274,12 +265,12 @@ struct MfmaTile<KvFormat::F16> {
         for (int blk = 0; blk < 2; ++blk) {
             const long row = row_base + min(t0 + 16 * blk + c, t_last);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) k[blk][ks] = load16(kp + row * kHeadDim + 32 * ks + 8 * g);
+            for (int ks = 0; ks < 4; ++ks) k[blk][ks] = stream16(kp + row * kHeadDim + 32 * ks + 8 * g);
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const long row = row_base + min(t0 + 8 * g + e, t_last);
-            v[e] = load16(vp + row * kHeadDim + 8 * c);
+            v[e] = stream16(vp + row * kHeadDim + 8 * c);
         }
     }
     __device__ __forceinline__ f16x8 kop(int blk, int ks) const { return as_f16x8(k[blk][ks]); }
@@ -313,14 +304,14 @@ struct MfmaTile<KvFormat::I8> {
         for (int blk = 0; blk < 2; ++blk) {
             const long row = row_base + min(t0 + 16 * blk + c, t_last);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) k[blk][u] = load16(kp + row * kHeadDim + 64 * u + 16 * g);
+            for (int u = 0; u < 2; ++u) k[blk][u] = stream16(kp + row * kHeadDim + 64 * u + 16 * g);
             ks[blk] = p.k_scale[row];
             vs[blk] = p.v_scale[row];
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const long row = row_base + min(t0 + 8 * g + e, t_last);
-            v[e] = load8(vp + row * kHeadDim + 8 * c);
+            v[e] = stream8(vp + row * kHeadDim + 8 * c);
         }
     }
     __device__ __forceinline__ f16x8 kop(int blk, int ks_) const {
@@ -360,13 +351,13 @@ struct MfmaTile<KvFormat::I4> {
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
             const long row = row_base + min(t0 + 16 * blk + c, t_last);
-            k[blk] = load16(kp + row * (kHeadDim / 2) + 16 * g);
+            k[blk] = stream16(kp + row * (kHeadDim / 2) + 16 * g);
             vs[blk] = p.v_scale[row];
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const long row = row_base + min(t0 + 8 * g + e, t_last);
-            v[e] = load4(vp + row * (kHeadDim / 2) + 4 * c);
+            v[e] = stream4(vp + row * (kHeadDim / 2) + 4 * c);
         }
     }
     __device__ __forceinline__ f16x8 kop(int blk, int ks_) const {
@@ -542,20 +533,10 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_mfma_kernel(Att
         for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(j), o[j]);
     };
 
-    // Two tile buffers: the next tile's loads are in flight while the
-    // current tile is processed.
-    MfmaTile<F> ta, tb;
-    int t0 = w0;
-    if (t0 < w1) ta.load(p, row_base, t0, w1 - 1, g, c);
-    while (t0 < w1) {
-        const int t1 = t0 + kTile;
-        if (t1 < w1) tb.load(p, row_base, t1, w1 - 1, g, c);
-        step(ta, t0);
-        if (t1 >= w1) break;
-        const int t2 = t1 + kTile;
-        if (t2 < w1) ta.load(p, row_base, t2, w1 - 1, g, c);
-        step(tb, t1);
-        t0 = t2;
+    for (int t0 = w0; t0 < w1; t0 += kTile) {
+        MfmaTile<F> tile;
+        tile.load(p, row_base, t0, w1 - 1, g, c);
+        step(tile, t0);
     }
 
     // ---- merge the 4 wave states through LDS ----

@@ -139,10 +139,10 @@ __global__ __launch_bounds__(kGemmThreads) void w4a16_gemv_kernel(GemmParams p) 
         if (active) {
             uint32_t wv[COLS];
             if constexpr (COLS == 4) {
-                const u32x4 raw = load16(p.w + (long)kp * p.N + n0);
+                const u32x4 raw = stream16(p.w + (long)kp * p.N + n0);
                 wv[0] = raw[0]; wv[1] = raw[1]; wv[2] = raw[2]; wv[3] = raw[3];
             } else {
-                wv[0] = p.w[(long)kp * p.N + n0];
+                wv[0] = stream4(p.w + (long)kp * p.N + n0);
             }
 #pragma unroll
             for (int j = 0; j < COLS; ++j) {
