@@ -47,9 +47,9 @@ namespace llmik {
 
 enum class KvFormat { F16, I8, I4 };
 
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 256;   // VALU kernel
 constexpr int kHeadDim = 128;
-constexpr int kChunkStep = 128;   // split sizes are multiples of this
+constexpr int kTile = 32;   // tokens per wave step of the MFMA kernel
 #ifndef LLMIK_ATTN_WGS_PER_CU
 #define LLMIK_ATTN_WGS_PER_CU 1
 #endif
@@ -76,20 +76,20 @@ struct AttnParams {
 // Shared tail: merge NR partial states held in LDS, then either write the
 // output (single split) or publish the split and let the last one combine.
 // ---------------------------------------------------------------------------
-template <int NR, int HPW>
+template <int NR, int HPW, int NT>
 __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*s_o)[HPW][kHeadDim],
                                              const float (*s_m)[HPW], const float (*s_l)[HPW],
                                              uint32_t* s_last, int b, int kvh, int hchunk,
                                              int split, int head0) {
     const int tid = threadIdx.x;
     constexpr int kOuts = HPW * kHeadDim;
-    constexpr int kPer = (kOuts + kAttnThreads - 1) / kAttnThreads;
+    constexpr int kPer = (kOuts + NT - 1) / NT;
     const int slot_group = (b * p.n_kv_heads + kvh) * p.n_hchunks + hchunk;
     const long slot = (long)slot_group * p.n_splits + split;
     float wo[kPer], wm[kPer], wl[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-        const int idx = tid + i * kAttnThreads;
+        const int idx = tid + i * NT;
         wo[i] = 0.0f;
         wm[i] = -INFINITY;
         wl[i] = 0.0f;
@@ -117,7 +117,7 @@ __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*
     if (p.n_splits == 1) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int idx = tid + i * kAttnThreads;
+            const int idx = tid + i * NT;
             if (idx < kOuts) {
                 const int h = idx / kHeadDim, d = idx % kHeadDim;
                 const float inv = (wl[i] > 0.0f) ? 1.0f / wl[i] : 0.0f;
@@ -129,7 +129,7 @@ __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*
 
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-        const int idx = tid + i * kAttnThreads;
+        const int idx = tid + i * NT;
         if (idx < kOuts) {
             const int h = idx / kHeadDim, d = idx % kHeadDim;
             publish_store(&p.part_o[(slot * HPW + h) * kHeadDim + d], wo[i]);
@@ -147,44 +147,59 @@ __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*
 
     // Last split of this (batch, kv head, head chunk): combine all splits.
     // Each thread issues the (m, l) and partial-output loads of a batch of
-    // splits together, so a combine of up to kBatch splits costs one memory
-    // round trip; rescaling to a common maximum is done in registers.
-    constexpr int kBatch = 16;
+    // splits for all of its outputs together, so a combine of up to kBatch
+    // splits costs one memory round trip; rescaling to a common maximum is
+    // done in registers.
+    constexpr int kBatch = (kPer == 1) ? 16 : 8;
     const long base = (long)slot_group * p.n_splits;
+    float gm[kPer], so[kPer], sl[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-        const int idx = tid + i * kAttnThreads;
+        gm[i] = -INFINITY;
+        so[i] = 0.0f;
+        sl[i] = 0.0f;
+    }
+    for (int sp0 = 0; sp0 < p.n_splits; sp0 += kBatch) {
+        float mv[kPer][kBatch], lv[kPer][kBatch], ov[kPer][kBatch];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = min(tid + i * NT, kOuts - 1);
+            const int h = idx / kHeadDim, d = idx % kHeadDim;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const long sl_idx = (base + min(sp0 + u, p.n_splits - 1)) * HPW + h;
+                mv[i][u] = publish_load(&p.part_ml[sl_idx * 2]);
+                lv[i][u] = publish_load(&p.part_ml[sl_idx * 2 + 1]);
+                ov[i][u] = publish_load(&p.part_o[sl_idx * kHeadDim + d]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            float bm = gm[i];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (sp0 + u < p.n_splits) bm = fmaxf(bm, mv[i][u]);
+            if (bm == -INFINITY) continue;
+            const float r = (gm[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(gm[i] - bm);
+            so[i] *= r;
+            sl[i] *= r;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const float w = (sp0 + u < p.n_splits && mv[i][u] != -INFINITY)
+                                    ? __builtin_amdgcn_exp2f(mv[i][u] - bm) : 0.0f;
+                so[i] = fmaf(ov[i][u], w, so[i]);
+                sl[i] = fmaf(lv[i][u], w, sl[i]);
+            }
+            gm[i] = bm;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = tid + i * NT;
         if (idx < kOuts) {
             const int h = idx / kHeadDim, d = idx % kHeadDim;
-            float gm = -INFINITY, so = 0.0f, sl = 0.0f;
-            for (int sp0 = 0; sp0 < p.n_splits; sp0 += kBatch) {
-                float mv[kBatch], lv[kBatch], ov[kBatch];
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const long sl_idx = (base + min(sp0 + u, p.n_splits - 1)) * HPW + h;
-                    mv[u] = publish_load(&p.part_ml[sl_idx * 2]);
-                    lv[u] = publish_load(&p.part_ml[sl_idx * 2 + 1]);
-                    ov[u] = publish_load(&p.part_o[sl_idx * kHeadDim + d]);
-                }
-                float bm = gm;
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u)
-                    if (sp0 + u < p.n_splits) bm = fmaxf(bm, mv[u]);
-                if (bm == -INFINITY) continue;
-                const float r = (gm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(gm - bm);
-                so *= r;
-                sl *= r;
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const float w = (sp0 + u < p.n_splits && mv[u] != -INFINITY)
-                                        ? __builtin_amdgcn_exp2f(mv[u] - bm) : 0.0f;
-                    so = fmaf(ov[u], w, so);
-                    sl = fmaf(lv[u], w, sl);
-                }
-                gm = bm;
-            }
-            const float inv = (sl > 0.0f) ? 1.0f / sl : 0.0f;
-            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so * inv);
+            const float inv = (sl[i] > 0.0f) ? 1.0f / sl[i] : 0.0f;
+            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so[i] * inv);
         }
     }
     if (tid == 0) p.counters[slot_group] = 0u;   // leave the counter zeroed for the next call
@@ -194,8 +209,6 @@ __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*
 // MFMA kernel
 // ===========================================================================
 
-constexpr int kMfmaWaves = kAttnThreads / kWave;   // 4
-constexpr int kTile = 32;                          // tokens per wave step
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const f16x8 a, const f16x8 b, const f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -383,8 +396,13 @@ struct MfmaTile<KvFormat::I4> {
     }
 };
 
-template <KvFormat F, int HPW>
-__global__ __launch_bounds__(kAttnThreads) void decode_attention_mfma_kernel(AttnParams p) {
+// NW waves per workgroup. fp16 / INT8: the waves take the split's 32-token
+// tiles round robin, so the workgroup streams one contiguous region and its
+// waves finish within a tile of each other. INT4: each wave takes a
+// contiguous quarter / eighth of the split, so its K-scale group changes
+// only every group_size tokens.
+template <KvFormat F, int HPW, int NW>
+__global__ __launch_bounds__(NW * kWave) void decode_attention_mfma_kernel(AttnParams p) {
     const int split = blockIdx.x;
     const int kvh = blockIdx.y / p.n_hchunks;
     const int hchunk = blockIdx.y % p.n_hchunks;
@@ -429,13 +447,21 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_mfma_kernel(Att
         l[i] = 0.0f;
     }
 
-    __shared__ __attribute__((aligned(16))) uint16_t s_p[kMfmaWaves][4][kTile];
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][4][kTile];
 
     const int t_begin = split * p.chunk;
     const int t_end = min(t_begin + p.chunk, p.seqlen);
-    const int per_wave = p.chunk / kMfmaWaves;   // multiple of kTile
-    const int w0 = min(t_begin + wave * per_wave, t_end);
-    const int w1 = min(w0 + per_wave, t_end);
+    constexpr bool kInterleave = (F != KvFormat::I4);
+    constexpr int kWaveStride = kInterleave ? NW * kTile : kTile;
+    int w0, w1;
+    if constexpr (kInterleave) {
+        w0 = t_begin + wave * kTile;
+        w1 = t_end;
+    } else {
+        const int per_wave = p.chunk / NW;   // multiple of kTile
+        w0 = min(t_begin + wave * per_wave, t_end);
+        w1 = min(w0 + per_wave, t_end);
+    }
     int cur_group = -1;
 
     auto step = [&](const MfmaTile<F>& tile, const int t0) {
@@ -533,9 +559,13 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_mfma_kernel(Att
         for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(j), o[j]);
     };
 
-    for (int t0 = w0; t0 < w1; t0 += kTile) {
+    for (int t0 = w0; t0 < w1; t0 += kWaveStride) {
         MfmaTile<F> tile;
         tile.load(p, row_base, t0, w1 - 1, g, c);
+        // Keep the V loads next to the K loads: the scheduler would otherwise
+        // sink them below the QK products, which costs a second memory round
+        // trip per tile.
+        __builtin_amdgcn_sched_barrier(0);
         step(tile, t0);
     }
 
@@ -543,9 +573,9 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_mfma_kernel(Att
 #pragma unroll
     for (int i = 0; i < 4; ++i) l[i] = row16_sum(l[i]);
 
-    __shared__ float s_o[kMfmaWaves][HPW][kHeadDim];
-    __shared__ float s_m[kMfmaWaves][HPW];
-    __shared__ float s_l[kMfmaWaves][HPW];
+    __shared__ float s_o[NW][HPW][kHeadDim];
+    __shared__ float s_m[NW][HPW];
+    __shared__ float s_l[NW][HPW];
     __shared__ uint32_t s_last;
     constexpr float kInvP = 1.0f / MfmaTile<F>::kPScale;
     if (g == 0) {
@@ -562,7 +592,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_mfma_kernel(Att
         }
     }
     __syncthreads();
-    finish_split<kMfmaWaves, HPW>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
+    finish_split<NW, HPW, NW * kWave>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
 }
 
 // ===========================================================================
@@ -751,7 +781,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_valu_kernel(Att
         }
     }
     __syncthreads();
-    finish_split<kRows, HPW>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
+    finish_split<kRows, HPW, kAttnThreads>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
 }
 
 // ---------------------------------------------------------------------------
@@ -775,18 +805,22 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
     pl.n_hchunks = gqa / pl.hpw;
     const long base_wgs = (long)batch * n_kv_heads * pl.n_hchunks;
     const int cus = device_cu_count();
-    // Aim for kAttnWgsPerCu workgroups per CU; every split gets at least
-    // one 128-token step (32 tokens per wave).
+    // Aim for kAttnWgsPerCu workgroups per CU. Calls that must split the
+    // sequence to fill the chip use 8-wave workgroups (more loads in flight
+    // per CU, one combine output per thread); otherwise 4 waves. Every split
+    // gets at least one 32-token tile per wave.
     const long target = (long)kAttnWgsPerCu * cus;
+    pl.waves = (base_wgs < target) ? 8 : 4;
+    const int step = kTile * pl.waves;
     long want = (target + base_wgs - 1) / base_wgs;
-    const long max_useful = (seqlen + kChunkStep - 1) / kChunkStep;
+    const long max_useful = (seqlen + step - 1) / step;
     if (want > max_useful) want = max_useful;
     if (want > kMaxAttnSplits) want = kMaxAttnSplits;
     if (base_wgs > kMaxCounters) want = 1;   // enough workgroups without splitting
     if (want < 1) want = 1;
     int chunk = (int)((seqlen + want - 1) / want);
-    chunk = ((chunk + kChunkStep - 1) / kChunkStep) * kChunkStep;
-    if (chunk < kChunkStep) chunk = kChunkStep;
+    chunk = ((chunk + step - 1) / step) * step;
+    if (chunk < step) chunk = step;
     pl.chunk = chunk;
     pl.n_splits = seqlen > 0 ? (seqlen + chunk - 1) / chunk : 1;
     pl.n_slot_groups = base_wgs;
@@ -800,9 +834,12 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
 }
 
 template <KvFormat F, int HPW>
-static void launch_kernel(const AttnParams& p, dim3 grid, bool mfma, hipStream_t stream) {
-    if (mfma) {
-        hipLaunchKernelGGL((decode_attention_mfma_kernel<F, HPW>), grid, dim3(kAttnThreads), 0,
+static void launch_kernel(const AttnParams& p, dim3 grid, bool mfma, int waves, hipStream_t stream) {
+    if (mfma && waves == 8) {
+        hipLaunchKernelGGL((decode_attention_mfma_kernel<F, HPW, 8>), grid, dim3(8 * kWave), 0,
+                           stream, p);
+    } else if (mfma) {
+        hipLaunchKernelGGL((decode_attention_mfma_kernel<F, HPW, 4>), grid, dim3(4 * kWave), 0,
                            stream, p);
     } else {
         hipLaunchKernelGGL((decode_attention_valu_kernel<F, HPW>), grid, dim3(kAttnThreads), 0,
@@ -843,9 +880,9 @@ static int launch_attention(const AttnLaunch& a, hipStream_t stream) {
     const bool mfma = (F != KvFormat::I4) || (p.group_size % 16 == 0);
     dim3 grid(pl.n_splits, a.n_kv_heads * pl.n_hchunks, a.batch);
     switch (pl.hpw) {
-        case 4: launch_kernel<F, 4>(p, grid, mfma, stream); break;
-        case 2: launch_kernel<F, 2>(p, grid, mfma, stream); break;
-        default: launch_kernel<F, 1>(p, grid, mfma, stream); break;
+        case 4: launch_kernel<F, 4>(p, grid, mfma, pl.waves, stream); break;
+        case 2: launch_kernel<F, 2>(p, grid, mfma, pl.waves, stream); break;
+        default: launch_kernel<F, 1>(p, grid, mfma, pl.waves, stream); break;
     }
     return check_launch();
 }

@@ -31,7 +31,8 @@ struct AttnPlan {
     int hpw;             // query heads per workgroup
     int n_hchunks;       // head chunks per kv head
     int n_splits;        // KV splits per (batch, kv head, head chunk)
-    int chunk;           // tokens per split (multiple of the 64-token step)
+    int chunk;           // tokens per split (multiple of 32 * waves)
+    int waves;           // waves per MFMA workgroup (4 or 8)
     long n_slot_groups;  // batch * n_kv_heads * n_hchunks
     size_t workspace_bytes;
     size_t off_ml, off_o;
