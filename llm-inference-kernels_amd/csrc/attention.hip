@@ -216,15 +216,6 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const f16x8 a, const f16x8 b, cons
 
 __device__ __forceinline__ f16x8 as_f16x8(const u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 
-__device__ __forceinline__ u32x4 make_u32x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    u32x4 r;
-    r[0] = a; r[1] = b; r[2] = c; r[3] = d;
-    return r;
-}
-
-__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
-    return __builtin_amdgcn_perm(hi, lo, sel);
-}
 
 // Two biased int8 bytes (value + 128, in bytes 0 and 2 of x, bytes 1 and 3
 // zero) -> two exact fp16 values: 0x6400 | u is 1024 + u.

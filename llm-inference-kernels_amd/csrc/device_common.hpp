@@ -60,6 +60,40 @@ __device__ __forceinline__ uint16_t f2h_bits(float x) {
     return __builtin_bit_cast(uint16_t, (f16)x);  // v_cvt_f16_f32, RNE
 }
 
+// Raw buffer resource over `bytes` bytes at `p` (gfx9 data-format word).
+// Loads through it take a 32-bit per-lane offset plus a uniform offset, and
+// return 0 beyond `bytes`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// 4-byte buffer load, non-temporal (streamed once).
+__device__ __forceinline__ uint32_t buffer_stream4(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                   uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 2);
+}
+
+__device__ __forceinline__ u32x4 make_u32x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    u32x4 r;
+    r[0] = a; r[1] = b; r[2] = c; r[3] = d;
+    return r;
+}
+
+// A constant materialised in a VGPR (a VALU op can read one scalar
+// constant only; a VGPR copy lets three-operand bit ops take two).
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t k) {
+    uint32_t v;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "i"(k));
+    return v;
+}
+
+// Byte permute: selector bytes 0-3 pick bytes of `lo`, 4-7 bytes of `hi`,
+// 0x0C gives 0x00 (v_perm_b32).
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
 // NOTE: __builtin_bit_cast applied directly to an ext-vector element
 // (`__builtin_bit_cast(f16x2, v[i])`) is miscompiled by this hipcc (every
 // element reads as element 0). Always copy the element to a scalar first.

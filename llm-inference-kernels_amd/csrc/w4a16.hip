@@ -32,6 +32,7 @@ struct GemmParams {
     int M, N, K, group_size;
     int splits, kp_per_split, n_tiles;
     int f32_out;
+    int gshift;          // log2(group_size / 32) on the matrix-core GEMV
 };
 
 // Eight int4 codes of one word -> four fp16 pairs, exact. Pair j holds the
@@ -206,6 +207,311 @@ __global__ __launch_bounds__(kGemmThreads) void w4a16_gemv_kernel(GemmParams p) 
 }
 
 // ---------------------------------------------------------------------------
+// M == 1 on the matrix cores (group_size a power of two >= 32).
+//
+// Work unit: a tile of 16 * CB columns and one K split. The grid is laid
+// out so that each XCD (workgroup id mod 8) takes a contiguous run of tiles:
+// neighbouring column strips of a packed row are then read by one L2 at
+// about the same time. Within a workgroup, kGemvWaves waves own whole
+// batches of the split's 32-K steps and are summed in LDS; with several
+// splits the last split of a tile adds the partials in split order.
+//
+// In a 16x16x32 MFMA the B operand of a lane is one packed word: 8 K
+// positions of one column. Lane l loads CB adjacent words of packed row
+// 4 * step + (l >> 4), columns n0 + CB * (l & 15) + j, and feeds word j to
+// MFMA j (columns j, j + CB, j + 2CB, ... of the tile).
+//
+// The word goes into the MFMA still biased: with u = code + 8, the low
+// nibbles (even K offsets i) become the fp16 value 1024 + u and the high
+// nibbles (odd i) 1024 + 16u (exact bit patterns 0x6400 | u, 0x6400 | u<<4),
+// in the pair order (i0,i4), (i1,i5), (i2,i6), (i3,i7). The activation is
+// staged per workgroup in LDS in that order, with odd offsets divided by 16
+// (exact), so for each K position the product is
+//   even: a (1024 + u)        = a * code + 1032 a
+//   odd : (a / 16)(1024 + 16u) = a * code +   72 a
+// and a 32-K step of the MFMA yields sum(a * code) + corr[step], with
+// corr[step] = 1032 * sum_even(a) + 72 * sum_odd(a) staged beside it. Each
+// step lies inside one scale group: acc += scale[g][n] * (t - corr[step]).
+// Every row of the 16x16 product is the same; row 0 is used.
+//
+// Loads: the activation loads of all waves are issued first, then each
+// wave's first two batches (weight words and group scales) before the
+// activation is staged, later batches one batch ahead of use (ping-pong). Step and group indices are clamped to the tensors, so
+// every load stays in bounds; steps past the split meet a zero-padded
+// activation and add 0.
+// ---------------------------------------------------------------------------
+#ifndef LLMIK_GEMV_CB
+#define LLMIK_GEMV_CB 2           // words per lane per step: tile = 16 * CB columns
+#endif
+#ifndef LLMIK_GEMV_WGS_PER_CU
+#define LLMIK_GEMV_WGS_PER_CU 1   // K splits are added until tiles * splits reaches this per CU
+#endif
+constexpr int kGemvWaves = 8;
+constexpr int kGemvThreads = kGemvWaves * kWave;
+constexpr int kGemvBatch = 8;          // 32-K steps per load batch (256 * CB bytes per step)
+constexpr int kGemvMaxK = 16384;        // K per split: activation and corrections in LDS
+constexpr int kGemvMaxStage = kGemvMaxK / 8 / kGemvThreads;
+
+// LDS bytes for a split of `sps` steps with `sb`-step batches: activation
+// (plus one zero batch) in fp16, per-chunk and per-step corrections in fp32.
+__host__ __device__ constexpr size_t gemv_lds_bytes(int sps, int sb) {
+    return (size_t)(sps + sb) * 64 + (size_t)sps * 16 + (size_t)(sps + sb) * 4;
+}
+
+template <int N_>
+struct UIntVec;
+template <> struct UIntVec<1> { using T = uint32_t; };
+template <> struct UIntVec<2> { using T = u32x2; };
+template <> struct UIntVec<4> { using T = u32x4; };
+
+template <int CB>
+__device__ __forceinline__ typename UIntVec<CB>::T buffer_load_words(__amdgpu_buffer_rsrc_t r,
+                                                                     uint32_t voff, uint32_t soff) {
+    if constexpr (CB == 1) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 2);
+    else if constexpr (CB == 2) return __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 2);
+    else return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2);
+}
+
+template <int CB>
+__device__ __forceinline__ uint32_t word_of(const typename UIntVec<CB>::T& v, int j) {
+    if constexpr (CB == 1) return v;
+    else return v[j];
+}
+
+// Weight words and scales of one batch of SB steps. GSHIFT = min(log2 of
+// steps per group, log2 SB): the batch touches NG groups; a group's scales
+// for the lane's CB columns are CB adjacent fp16.
+template <int CB, int GSHIFT>
+struct GemvBatch {
+    static constexpr int SB = kGemvBatch;
+    static constexpr int NG = SB >> GSHIFT;
+    static constexpr int SW = (CB + 1) / 2;   // dwords of CB fp16 scales
+    typename UIntVec<CB>::T w[SB];
+    typename UIntVec<SW>::T s[NG];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs,
+                                         uint32_t w_off, uint32_t s_off, uint32_t step_bytes,
+                                         uint32_t grp_bytes, int step0, int last_step,
+                                         int gshift, int last_grp) {
+        // Steps past the split's last one re-read that step (same CU, cached).
+#pragma unroll
+        for (int j = 0; j < SB; ++j)
+            w[j] = buffer_load_words<CB>(rw, w_off, (uint32_t)min(step0 + j, last_step) * step_bytes);
+        const int g0 = step0 >> gshift;
+#pragma unroll
+        for (int u = 0; u < NG; ++u) {
+            const uint32_t so = (uint32_t)min(g0 + u, last_grp) * grp_bytes;
+            if constexpr (CB == 1) s[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)so, 0);
+            else s[u] = buffer_load_words<SW>(rs, s_off, so);
+        }
+    }
+    __device__ __forceinline__ float scale(int j, int cb) const {
+        const int u = j >> GSHIFT;
+        uint32_t d;
+        if constexpr (CB == 1) d = s[u];
+        else d = word_of<SW>(s[u], cb >> 1);
+        return h2f((uint16_t)((cb & 1) ? (d >> 16) : d));
+    }
+};
+
+// MULTI: every wave owns more than one batch (the host knows from the
+// plan). The two paths issue a fixed number of loads before the staging, so
+// the wait for the activation never includes weight loads.
+template <int CB, int NSTAGE, int GSHIFT, bool MULTI>
+__global__ __launch_bounds__(kGemvThreads) void w4a16_gemv_mfma_kernel(GemmParams p) {
+    constexpr int SB = kGemvBatch;
+    constexpr int TN = 16 * CB;
+    extern __shared__ __attribute__((aligned(16))) uint16_t s_dyn[];
+    __shared__ float s_red[kGemvWaves][TN];
+    __shared__ uint32_t s_last;
+
+    // XCD-contiguous order: workgroup b runs on XCD b % 8.
+    int b = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
+    const int tile = b % p.n_tiles;
+    const int split = b / p.n_tiles;
+
+    const int steps = p.K / 32;
+    const int sps = p.kp_per_split / 4;          // steps per split, a multiple of SB
+    const int k0 = split * sps;
+    const int nst = min(sps, steps - k0);        // steps of this split
+    uint16_t* s_act = s_dyn;                                                 // [sps + SB][32]
+    float* s_cchunk = reinterpret_cast<float*>(s_dyn + 32 * (sps + SB));     // [4 * sps]
+    float* s_corr = s_cchunk + 4 * sps;                                      // [sps + SB]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15;
+    const int kq = lane >> 4;
+    const int n0 = tile * TN;
+    const int col0 = n0 + CB * c;
+
+    // ---- activation staging loads first (the split's 8-element chunks) ----
+    const int n_act = 4 * nst;
+    const uint16_t* act = p.act + 32 * k0;
+    u32x4 stage[NSTAGE];
+#pragma unroll
+    for (int i = 0; i < NSTAGE; ++i)
+        stage[i] = load16(act + 8 * min((int)threadIdx.x + i * kGemvThreads, n_act - 1));
+
+    // Every wave's activation loads enter the CU's memory pipeline before any
+    // weight load (a bare barrier: it waits for no memory counter), so the
+    // staging does not queue behind other waves' weight streams.
+    __builtin_amdgcn_s_barrier();
+
+    // ---- then the wave's first two batches ----
+    const int per_wave = p.kp_per_split / 4 / kGemvWaves;   // whole batches, same for all waves
+    const int s0 = wave * per_wave;                          // past nst in a short last split
+    const int s1 = min(s0 + per_wave, nst);
+    const int last = k0 + nst - 1;
+    const int n_grp = p.K / p.group_size;
+    const __amdgpu_buffer_rsrc_t rw = make_buffer_rsrc(p.w, (uint32_t)(p.K / 8) * p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rs = make_buffer_rsrc(p.scale, (uint32_t)n_grp * p.N * 2u);
+    const uint32_t w_off = ((uint32_t)kq * p.N + col0) * 4u;
+    const uint32_t s_off = (uint32_t)col0 * 2u;
+    const uint32_t step_bytes = (uint32_t)p.N * 16u;
+    const uint32_t grp_bytes = (uint32_t)p.N * 2u;
+    GemvBatch<CB, GSHIFT> ba, bb;
+    ba.load(rw, rs, w_off, s_off, step_bytes, grp_bytes, k0 + s0, last, p.gshift, n_grp - 1);
+    if constexpr (MULTI)
+        bb.load(rw, rs, w_off, s_off, step_bytes, grp_bytes, k0 + s0 + SB, last, p.gshift, n_grp - 1);
+
+    // ---- stage the activation in pair order, odd offsets / 16 ----
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+#pragma unroll
+    for (int i = 0; i < NSTAGE; ++i) {
+        const int idx = (int)threadIdx.x + i * kGemvThreads;
+        if (idx < n_act) {
+            const u32x4 a = stage[i];
+            const f16x2 odd0 = as_f16x2(perm_b32(a[2], a[0], 0x07060302u)) * sixteenth;   // a1 a5
+            const f16x2 odd1 = as_f16x2(perm_b32(a[3], a[1], 0x07060302u)) * sixteenth;   // a3 a7
+            u32x4 r;
+            r[0] = perm_b32(a[2], a[0], 0x05040100u);   // a0 a4
+            r[1] = __builtin_bit_cast(uint32_t, odd0);
+            r[2] = perm_b32(a[3], a[1], 0x05040100u);   // a2 a6
+            r[3] = __builtin_bit_cast(uint32_t, odd1);
+            *reinterpret_cast<u32x4*>(&s_act[8 * idx]) = r;
+            float av[8];
+            f16x8_to_f32(a, av);
+            s_cchunk[idx] = 1032.0f * ((av[0] + av[2]) + (av[4] + av[6])) +
+                            72.0f * ((av[1] + av[3]) + (av[5] + av[7]));
+        }
+    }
+    // zero padding: activation and corrections of the steps [nst, nst + SB)
+    for (int t = threadIdx.x; t < 4 * SB; t += kGemvThreads)
+        *reinterpret_cast<u32x4*>(&s_act[32 * nst + 8 * t]) = u32x4{0u, 0u, 0u, 0u};
+    if ((int)threadIdx.x < SB) s_corr[nst + threadIdx.x] = 0.0f;
+    __syncthreads();
+    for (int st = threadIdx.x; st < nst; st += kGemvThreads) {
+        const float* q = s_cchunk + 4 * st;
+        s_corr[st] = (q[0] + q[1]) + (q[2] + q[3]);
+    }
+    __syncthreads();
+
+    // The masks and the exponent bits live in VGPRs so that each
+    // (word & mask) | bias is a single three-operand bit op.
+    const uint32_t m_lo = vgpr_const(0x000F000Fu);
+    const uint32_t m_hi = vgpr_const(0x00F000F0u);
+    const uint32_t bias = vgpr_const(0x64006400u);
+    float acc[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) acc[j] = 0.0f;
+    auto consume = [&](const GemvBatch<CB, GSHIFT>& bt, int b0) {
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            const int st = b0 + j;
+            const f16x8 aop = __builtin_bit_cast(
+                f16x8, *reinterpret_cast<const u32x4*>(&s_act[32 * st + 8 * kq]));
+            const float corr = s_corr[st];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const uint32_t w = word_of<CB>(bt.w[j], cb) ^ 0x88888888u;
+                const uint32_t w8 = w >> 8;
+                const u32x4 braw = make_u32x4((w & m_lo) | bias, (w & m_hi) | bias,
+                                              (w8 & m_lo) | bias, (w8 & m_hi) | bias);
+                const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    aop, __builtin_bit_cast(f16x8, braw), f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                acc[cb] = fmaf(bt.scale(j, cb), t[0] - corr, acc[cb]);
+            }
+        }
+    };
+    if constexpr (!MULTI) {
+        if (s0 < s1) consume(ba, s0);
+    } else if (s0 < s1) {
+        for (int b0 = s0;; b0 += 2 * SB) {
+            consume(ba, b0);
+            if (b0 + SB >= s1) break;
+            // Issued unconditionally (clamped) so the wait before each use stays exact.
+            ba.load(rw, rs, w_off, s_off, step_bytes, grp_bytes, k0 + b0 + 2 * SB, last, p.gshift,
+                    n_grp - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(bb, b0 + SB);
+            if (b0 + 2 * SB >= s1) break;
+            bb.load(rw, rs, w_off, s_off, step_bytes, grp_bytes, k0 + b0 + 3 * SB, last, p.gshift,
+                    n_grp - 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    if (kq == 0) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) s_red[wave][CB * c + cb] = acc[cb];
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    float v = 0.0f;
+    if (t < TN) {
+#pragma unroll
+        for (int w = 0; w < kGemvWaves; ++w) v += s_red[w][t];
+    }
+    if (p.splits == 1) {
+        if (t < TN) store_out(p, 0, n0 + t, v);
+        return;
+    }
+    if (t < TN) publish_store(&p.part[(long)split * p.N + n0 + t], v);
+    publish_wait();
+    __syncthreads();
+    if (t == 0) s_last = arrive_last(&p.counters[tile], (uint32_t)p.splits) ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u) return;
+    if (t < TN) store_out(p, 0, n0 + t, sum_splits(p.part + n0 + t, (long)p.N, p.splits));
+    if (t == 0) p.counters[tile] = 0u;
+}
+
+template <int CB, int NSTAGE, bool MULTI>
+static void launch_gemv_cb_stage(const GemmParams& p, int grid, size_t lds, hipStream_t stream) {
+    const dim3 g(grid), blk(kGemvThreads);
+    switch (min(p.gshift, 3)) {   // 3 = log2(kGemvBatch): a batch inside one group
+        case 0: hipLaunchKernelGGL((w4a16_gemv_mfma_kernel<CB, NSTAGE, 0, MULTI>), g, blk, lds, stream, p); break;
+        case 1: hipLaunchKernelGGL((w4a16_gemv_mfma_kernel<CB, NSTAGE, 1, MULTI>), g, blk, lds, stream, p); break;
+        case 2: hipLaunchKernelGGL((w4a16_gemv_mfma_kernel<CB, NSTAGE, 2, MULTI>), g, blk, lds, stream, p); break;
+        default: hipLaunchKernelGGL((w4a16_gemv_mfma_kernel<CB, NSTAGE, 3, MULTI>), g, blk, lds, stream, p); break;
+    }
+}
+
+template <int CB>
+static void launch_gemv_cb(const GemmParams& p, int grid, int sps, hipStream_t stream) {
+    const size_t lds = gemv_lds_bytes(sps, kGemvBatch);
+    const bool multi = sps / kGemvWaves > kGemvBatch;
+    const int stage = (4 * sps + kGemvThreads - 1) / kGemvThreads;
+    if (multi) {
+        switch (stage) {
+            case 1: launch_gemv_cb_stage<CB, 1, true>(p, grid, lds, stream); break;
+            case 2: launch_gemv_cb_stage<CB, 2, true>(p, grid, lds, stream); break;
+            case 3: launch_gemv_cb_stage<CB, 3, true>(p, grid, lds, stream); break;
+            default: launch_gemv_cb_stage<CB, kGemvMaxStage, true>(p, grid, lds, stream); break;
+        }
+    } else {
+        switch (stage) {
+            case 1: launch_gemv_cb_stage<CB, 1, false>(p, grid, lds, stream); break;
+            case 2: launch_gemv_cb_stage<CB, 2, false>(p, grid, lds, stream); break;
+            case 3: launch_gemv_cb_stage<CB, 3, false>(p, grid, lds, stream); break;
+            default: launch_gemv_cb_stage<CB, kGemvMaxStage, false>(p, grid, lds, stream); break;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // M > 1: each lane owns COLS columns and MT rows; the weight is dequantised
 // once per packed word into fp32 (code * scale, exact) and reused across the
 // MT rows. Grid z walks the row tiles.
@@ -371,6 +677,37 @@ __global__ __launch_bounds__(256) void w4a16_dequantize_kernel(const uint32_t* _
 
 GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     GemmPlan pl{};
+    const bool pow2_group = group_size >= 32 && (group_size & (group_size - 1)) == 0;
+    if (M == 1 && N % 16 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31)) {
+        // Matrix-core GEMV: widest tile (16 * cb columns) that divides N.
+        int cb = LLMIK_GEMV_CB;
+        while (cb > 1 && N % (16 * cb) != 0) cb /= 2;
+        const int sb = kGemvBatch * kGemvWaves;   // a split is whole batches for every wave
+        const int steps = K / 32;
+        const int tiles = N / (16 * cb);
+        const long target = (long)LLMIK_GEMV_WGS_PER_CU * device_cu_count();
+        long want = (target + tiles - 1) / tiles;
+        const long max_splits = (steps + sb - 1) / sb;
+        if (want > max_splits) want = max_splits;
+        if (tiles > kMaxCounters) want = 1;
+        if (want < 1) want = 1;
+        int sps = (int)((steps + want - 1) / want);
+        sps = (sps + sb - 1) / sb * sb;
+        if (sps * 32 <= kGemvMaxK) {
+            pl.kind = 2;
+            pl.cols_per_lane = cb;
+            pl.tile_n = 16 * cb;
+            pl.tile_m = 1;
+            pl.n_tiles = tiles;
+            pl.m_tiles = 1;
+            pl.kp_per_split = 4 * sps;
+            pl.splits = (steps + sps - 1) / sps;
+            pl.off_part = kCounterBytes;
+            pl.workspace_bytes =
+                (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * N * sizeof(float), 256) : 0;
+            return pl;
+        }
+    }
     pl.cols_per_lane = (N % 4 == 0) ? 4 : 1;
     pl.tile_n = 64 * pl.cols_per_lane;
     pl.n_tiles = (N + pl.tile_n - 1) / pl.tile_n;
@@ -419,8 +756,18 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
     p.kp_per_split = pl.kp_per_split;
     p.n_tiles = pl.n_tiles;
     p.f32_out = f32_out ? 1 : 0;
+    p.gshift = 0;
+    while ((32 << p.gshift) < group_size) ++p.gshift;
     dim3 block(kGemmThreads);
-    if (pl.kind == 0) {
+    if (pl.kind == 2) {
+        const int grid = pl.n_tiles * pl.splits;
+        const int sps = pl.kp_per_split / 4;
+        switch (pl.cols_per_lane) {
+            case 4: launch_gemv_cb<4>(p, grid, sps, stream); break;
+            case 2: launch_gemv_cb<2>(p, grid, sps, stream); break;
+            default: launch_gemv_cb<1>(p, grid, sps, stream); break;
+        }
+    } else if (pl.kind == 0) {
         dim3 grid(pl.n_tiles, pl.splits);
         if (pl.cols_per_lane == 4) hipLaunchKernelGGL(w4a16_gemv_kernel<4>, grid, block, 0, stream, p);
         else hipLaunchKernelGGL(w4a16_gemv_kernel<1>, grid, block, 0, stream, p);

@@ -100,7 +100,13 @@ def test_c_layer_argument_errors(lib):
 def test_workspace_sizes_without_gpu(lib):
     assert lib.llmik_attention_workspace_size(8, 32, 8, 4096, 128) > 0
     assert lib.llmik_attention_workspace_size(8, 32, 8, 4096, 64) == 0
-    assert lib.llmik_w4a16_workspace_size(1, 4096, 4096, 128) > 0
+    # Split-K plans need the counter region plus one fp32 partial per split
+    # and output; a plan without splits needs none.
+    for M, N, K, gs in [(1, 4096, 4096, 128), (1, 4096, 4096, 16), (16, 4096, 4096, 128),
+                        (1, 14336, 4096, 128)]:
+        ws = lib.llmik_w4a16_workspace_size(M, N, K, gs)
+        assert ws == 0 or (ws >= 16384 + M * N * 4 * 2 and ws % 256 == 0)
+    assert lib.llmik_w4a16_workspace_size(1, 4096, 4096, 16) > 0
 
 
 def test_op_surface_matches_reference(mod):

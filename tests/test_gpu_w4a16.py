@@ -62,7 +62,15 @@ def test_llama_shapes(llmik, cuda, M, K, N):
 
 @pytest.mark.parametrize("M,K,N,gs", [(1, 256, 64, 64), (3, 512, 100, 128), (1, 1024, 1000, 32),
                                       (5, 128, 4, 128), (17, 768, 96, 256), (1, 8192, 36, 128),
-                                      (33, 256, 260, 64)])
+                                      (33, 256, 260, 64),
+                                      # M == 1 matrix-core GEMV: fewest steps, idle waves,
+                                      # several load batches per wave
+                                      (1, 32, 16, 32), (1, 96, 48, 32), (1, 512, 32, 256),
+                                      (1, 16384, 32, 128),
+                                      # M == 1 split-K VALU GEMV: group below 32
+                                      # or not a power of two, K beyond the staged row
+                                      (1, 512, 128, 16), (1, 256, 64, 8), (1, 384, 32, 96),
+                                      (1, 20480, 32, 128)])
 def test_odd_shapes(llmik, cuda, M, K, N, gs):
     _check(llmik, cuda, M, K, N, gs, seed=M * 7 + K)
 
