@@ -40,6 +40,7 @@ sys.path.insert(0, str(ROOT / "llm-inference-kernels_amd"))
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "decode_attention_fp16_a16_traffic.md"
 MFMA_FP16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 768 << 20
 GATE_TOL = 2e-3
@@ -294,6 +295,50 @@ def cpu_baseline(budget_s: float = 15.0):
                       f"median; numpy BLAS threads={threads}"}
 
 
+# ------------------------------------------------------------- HBM traffic
+
+def pmc_workload(llmik, steps: int) -> None:
+    """The program the rocprofv3 --pmc passes run: the headline attention
+    call `steps` times, eagerly, over rotating HBM-resident input sets, then
+    five plain copies of 256 MiB (torch copy_, a read and a write of known
+    size) whose counter readings give the scale factor."""
+    import torch
+    dev = torch.device("cuda:0")
+    B, H, Hkv, S, D = 8, 32, 8, 4096, 128
+    n_sets = n_sets_for(attn_bytes("fp16", B, H, Hkv, S, D))
+    gen = torch.Generator(device=dev).manual_seed(1)
+    sets = [(torch.randn((B, H, D), generator=gen, device=dev, dtype=torch.float16),
+             torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16),
+             torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16))
+            for _ in range(n_sets)]
+    for i in range(steps):
+        llmik.decode_attention(*sets[i % n_sets], 1.0 / math.sqrt(D))
+    torch.cuda.synchronize()
+    del sets
+    src = torch.randint(0, 255, (256 << 20,), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc workload done: {steps} attention calls (B={B} S={S}), 5 x 256 MiB copies")
+
+
+def read_traffic():
+    """HBM bytes per headline launch from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy kernel's readings),
+    or None when the summary is absent."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    vals = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        parts = line.strip().strip("`").split()
+        if len(parts) == 2 and parts[0] in ("fetch_bytes_per_launch", "write_bytes_per_launch"):
+            vals[parts[0]] = int(parts[1])
+    if len(vals) != 2:
+        return None
+    return vals["fetch_bytes_per_launch"] + vals["write_bytes_per_launch"]
+
+
 # ---------------------------------------------------------------------- main
 
 def main() -> None:
@@ -304,6 +349,8 @@ def main() -> None:
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list: attn,int8,int4,w4a16,writers,sweep")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run the counter-collection program (headline calls + copies) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are out of scope "
@@ -315,6 +362,9 @@ def main() -> None:
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     log(f"device {torch.cuda.get_device_name(0)}; library {llmik.LIB_PATH}")
+    if args.pmc_workload:
+        pmc_workload(llmik, args.steps)
+        return
 
     only = set(filter(None, args.only.split(",")))
     want = (lambda k: not only or k in only)
@@ -372,7 +422,7 @@ def main() -> None:
                    "seqlen_kv": 4096, "kv_layout": "[B, Hkv, S, D] fp16 contiguous",
                    "input_sets_rotated": head["sets"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": head["bytes"]},
         "cpu_baseline": cpu,
         "details": details,
