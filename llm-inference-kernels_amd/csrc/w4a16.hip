@@ -512,6 +512,212 @@ static void launch_gemv_cb(const GemmParams& p, int grid, int sps, hipStream_t s
 }
 
 // ---------------------------------------------------------------------------
+// M >= 2 on the matrix cores (N % 64 == 0, group_size a power of two >= 32).
+//
+// A workgroup of 4 waves computes a tile of TM = 16 * RT rows by 64 columns
+// over one K split; wave w owns the 16-column block n0 + 16w. For each 32-K
+// step a lane dequantises one packed word (column n0 + 16w + (l & 15),
+// packed row 4 * step + (l >> 4)) to exact fp16 codes and feeds it as the B
+// operand to RT MFMAs, one per 16-row tile of the activation. The
+// activation rows of a chunk of KC steps are staged once per workgroup in
+// LDS, in the pair order of the dequantised word, and read by all four
+// waves; the next chunk is loaded into registers while the current one is
+// consumed. The step products accumulate in fp32 per scale group and are
+// scaled at the end of each group: acc += scale[g][n] * C_group.
+// ---------------------------------------------------------------------------
+constexpr int kMmaThreads = 256;
+
+template <int RT>
+struct MmaShape {
+    static constexpr int TM = 16 * RT;
+    static constexpr int KC = (RT >= 8) ? 4 : (RT >= 4 ? 8 : 16);   // steps per LDS chunk
+    static constexpr int A_LOADS = TM * KC * 4 / kMmaThreads;      // 16-byte loads per thread
+};
+
+template <int RT>
+__global__ __launch_bounds__(kMmaThreads) void w4a16_gemm_mfma_kernel(GemmParams p) {
+    using S = MmaShape<RT>;
+    constexpr int TM = S::TM, KC = S::KC;
+    __shared__ __attribute__((aligned(16))) uint16_t s_a[KC][TM][32];
+    __shared__ uint32_t s_last;
+
+    // (tile, split, m-tile) from an XCD-contiguous order of workgroup ids.
+    int b = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
+    const int tile = b % p.n_tiles;
+    const int rest = b / p.n_tiles;
+    const int split = rest % p.splits;
+    const int mtile = rest / p.splits;
+
+    const int steps = p.K / 32;
+    const int sps = p.kp_per_split / 4;
+    const int k0 = split * sps;
+    const int nst = min(sps, steps - k0);
+    const int m0 = mtile * TM;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15;
+    const int kq = lane >> 4;
+    const int n0 = tile * 64;
+    const int n = n0 + 16 * wave + c;
+
+    const int n_grp = p.K / p.group_size;
+    const int spg_mask = (1 << p.gshift) - 1;   // steps per group - 1
+    const __amdgpu_buffer_rsrc_t rw = make_buffer_rsrc(p.w, (uint32_t)(p.K / 8) * p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rs = make_buffer_rsrc(p.scale, (uint32_t)n_grp * p.N * 2u);
+    const uint32_t w_off = ((uint32_t)kq * p.N + n) * 4u;
+    const uint32_t s_off = (uint32_t)n * 2u;
+    const uint32_t step_bytes = (uint32_t)p.N * 16u;
+    const uint32_t grp_bytes = (uint32_t)p.N * 2u;
+    const int last = k0 + nst - 1;
+
+    // Activation chunk loads of this thread: chunk i covers steps
+    // [k0 + i*KC, ...); slot j -> (step, row, 8-value quarter).
+    u32x4 areg[S::A_LOADS];
+    auto load_a = [&](int chunk) {
+#pragma unroll
+        for (int j = 0; j < S::A_LOADS; ++j) {
+            const int idx = threadIdx.x + j * kMmaThreads;
+            const int st = idx / (TM * 4);
+            const int row = (idx >> 2) % TM;
+            const int qq = idx & 3;
+            const int gst = chunk * KC + st;            // step within the split
+            const int m = m0 + row;
+            const bool ok = (gst < nst) && (m < p.M);
+            const long off = (long)min(m, p.M - 1) * p.K + 32L * (k0 + min(gst, nst - 1)) + 8 * qq;
+            const u32x4 v = load16(p.act + off);
+            areg[j] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store_a = [&]() {
+#pragma unroll
+        for (int j = 0; j < S::A_LOADS; ++j) {
+            const int idx = threadIdx.x + j * kMmaThreads;
+            const int st = idx / (TM * 4);
+            const int row = (idx >> 2) % TM;
+            const int qq = idx & 3;
+            const u32x4 a = areg[j];
+            u32x4 r;
+            r[0] = perm_b32(a[2], a[0], 0x05040100u);   // a0 a4
+            r[1] = perm_b32(a[2], a[0], 0x07060302u);   // a1 a5
+            r[2] = perm_b32(a[3], a[1], 0x05040100u);   // a2 a6
+            r[3] = perm_b32(a[3], a[1], 0x07060302u);   // a3 a7
+            *reinterpret_cast<u32x4*>(&s_a[st][row][8 * qq]) = r;
+        }
+    };
+    // Weight words and scales of a chunk (clamped to the split: in bounds).
+    struct WChunk {
+        uint32_t w[KC];
+        uint32_t sc[KC];
+    };
+    auto load_w = [&](WChunk& wc, int chunk) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const int gs = min(k0 + chunk * KC + j, last);
+            wc.w[j] = buffer_stream4(rw, w_off, (uint32_t)gs * step_bytes);
+            wc.sc[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off,
+                                                            (int)((uint32_t)(gs >> p.gshift) * grp_bytes), 0);
+        }
+    };
+
+    f32x4 acc[RT], cg[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        acc[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        cg[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const int n_chunks = (nst + KC - 1) / KC;
+    WChunk wa, wb;
+    load_a(0);
+    load_w(wa, 0);
+    auto compute = [&](const WChunk& wc, int chunk) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const int sl = chunk * KC + j;              // step within the split
+            if (sl < nst) {
+                f16x2 wp[4];
+                i4x8_to_f16_pairs(wc.w[j], wp);
+                f16x8 bop;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bop[2 * i] = wp[i][0];
+                    bop[2 * i + 1] = wp[i][1];
+                }
+#pragma unroll
+                for (int r = 0; r < RT; ++r) {
+                    const f16x8 aop = __builtin_bit_cast(
+                        f16x8, *reinterpret_cast<const u32x4*>(&s_a[j][16 * r + c][8 * kq]));
+                    cg[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, cg[r], 0, 0, 0);
+                }
+                const int gst = k0 + sl;
+                if (((gst & spg_mask) == spg_mask) || sl == nst - 1) {   // end of a scale group
+                    const float scv = h2f((uint16_t)wc.sc[j]);
+#pragma unroll
+                    for (int r = 0; r < RT; ++r) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[r][i] = fmaf(scv, cg[r][i], acc[r][i]);
+                        cg[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+                }
+            }
+        }
+    };
+    for (int ch = 0; ch < n_chunks; ch += 2) {
+        __syncthreads();                 // previous chunk's reads of s_a are done
+        store_a();
+        __syncthreads();
+        if (ch + 1 < n_chunks) {
+            load_a(ch + 1);
+            load_w(wb, ch + 1);
+        }
+        compute(wa, ch);
+        if (ch + 1 >= n_chunks) break;
+        __syncthreads();
+        store_a();
+        __syncthreads();
+        if (ch + 2 < n_chunks) {
+            load_a(ch + 2);
+            load_w(wa, ch + 2);
+        }
+        compute(wb, ch + 1);
+    }
+
+    // C layout: lane (c, kq) holds rows 4kq..4kq+3 of each 16-row tile, column n.
+    auto out_index = [&](int r, int i) { return m0 + 16 * r + 4 * kq + i; };
+    if (p.splits == 1) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (out_index(r, i) < p.M) store_out(p, out_index(r, i), n, acc[r][i]);
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (out_index(r, i) < p.M)
+                publish_store(&p.part[((long)split * p.M + out_index(r, i)) * p.N + n], acc[r][i]);
+    publish_wait();
+    __syncthreads();
+    const int counter = mtile * p.n_tiles + tile;
+    if (threadIdx.x == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u) return;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = out_index(r, i);
+            if (m < p.M)
+                store_out(p, m, n, sum_splits(p.part + (long)m * p.N + n, (long)p.M * p.N, p.splits));
+        }
+    if (threadIdx.x == 0) p.counters[counter] = 0u;
+}
+
+// ---------------------------------------------------------------------------
 // M > 1: each lane owns COLS columns and MT rows; the weight is dequantised
 // once per packed word into fp32 (code * scale, exact) and reused across the
 // MT rows. Grid z walks the row tiles.
@@ -708,6 +914,34 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
             return pl;
         }
     }
+    if (M >= 2 && N % 64 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31)) {
+        // Matrix-core GEMM: tiles of 16 * rt rows by 64 columns.
+        int rt = 1;
+        while (rt < 8 && 16 * rt < M) rt *= 2;
+        const int kc = (rt >= 8) ? 4 : (rt >= 4 ? 8 : 16);
+        const int steps = K / 32;
+        pl.kind = 3;
+        pl.cols_per_lane = 1;
+        pl.tile_n = 64;
+        pl.tile_m = 16 * rt;
+        pl.n_tiles = N / 64;
+        pl.m_tiles = (M + pl.tile_m - 1) / pl.tile_m;
+        const long base = (long)pl.n_tiles * pl.m_tiles;
+        const long target = device_cu_count();
+        long want = (target + base - 1) / base;
+        const long max_splits = (steps + kc - 1) / kc;
+        if (want > max_splits) want = max_splits;
+        if (base > kMaxCounters) want = 1;
+        if (want < 1) want = 1;
+        int sps = (int)((steps + want - 1) / want);
+        sps = (sps + kc - 1) / kc * kc;
+        pl.kp_per_split = 4 * sps;
+        pl.splits = (steps + sps - 1) / sps;
+        pl.off_part = kCounterBytes;
+        pl.workspace_bytes =
+            (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
+        return pl;
+    }
     pl.cols_per_lane = (N % 4 == 0) ? 4 : 1;
     pl.tile_n = 64 * pl.cols_per_lane;
     pl.n_tiles = (N + pl.tile_n - 1) / pl.tile_n;
@@ -766,6 +1000,14 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
             case 4: launch_gemv_cb<4>(p, grid, sps, stream); break;
             case 2: launch_gemv_cb<2>(p, grid, sps, stream); break;
             default: launch_gemv_cb<1>(p, grid, sps, stream); break;
+        }
+    } else if (pl.kind == 3) {
+        const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kMmaThreads);
+        switch (pl.tile_m) {
+            case 16: hipLaunchKernelGGL(w4a16_gemm_mfma_kernel<1>, grid, blk, 0, stream, p); break;
+            case 32: hipLaunchKernelGGL(w4a16_gemm_mfma_kernel<2>, grid, blk, 0, stream, p); break;
+            case 64: hipLaunchKernelGGL(w4a16_gemm_mfma_kernel<4>, grid, blk, 0, stream, p); break;
+            default: hipLaunchKernelGGL(w4a16_gemm_mfma_kernel<8>, grid, blk, 0, stream, p); break;
         }
     } else if (pl.kind == 0) {
         dim3 grid(pl.n_tiles, pl.splits);

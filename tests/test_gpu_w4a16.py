@@ -70,7 +70,11 @@ def test_llama_shapes(llmik, cuda, M, K, N):
                                       # M == 1 split-K VALU GEMV: group below 32
                                       # or not a power of two, K beyond the staged row
                                       (1, 512, 128, 16), (1, 256, 64, 8), (1, 384, 32, 96),
-                                      (1, 20480, 32, 128)])
+                                      (1, 20480, 32, 128),
+                                      # M >= 2 matrix-core GEMM: row tiles 1/2/4/8, partial and
+                                      # several m tiles, one-step K, groups 32..256
+                                      (2, 1024, 128, 32), (17, 512, 192, 64), (33, 2048, 64, 256),
+                                      (100, 384, 128, 128), (200, 256, 64, 32), (7, 32, 64, 32)])
 def test_odd_shapes(llmik, cuda, M, K, N, gs):
     _check(llmik, cuda, M, K, N, gs, seed=M * 7 + K)
 
