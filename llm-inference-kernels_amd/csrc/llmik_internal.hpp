@@ -68,7 +68,8 @@ int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int ba
 // ---- W4A16 -----------------------------------------------------------------
 struct GemmPlan {
     int kind;          // 0: single-row VALU GEMV, 1: tiled multi-row VALU,
-                       // 2: single-row MFMA GEMV, 3: multi-row MFMA GEMM
+                       // 2: single-row MFMA GEMV, 3: multi-row MFMA GEMM,
+                       // 4: MFMA GEMV over up to 16 rows
     int cols_per_lane; // 4 (16-byte weight loads) or 1
     int tile_n;        // output columns per workgroup
     int tile_m;        // output rows per workgroup

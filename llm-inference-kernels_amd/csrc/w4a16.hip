@@ -512,6 +512,200 @@ static void launch_gemv_cb(const GemmParams& p, int grid, int sps, hipStream_t s
 }
 
 // ---------------------------------------------------------------------------
+// 2 <= M <= 16 on the matrix cores: the single-row GEMV's structure (16 * CB
+// column tiles, K splits, 8 waves on whole batches of 32-K steps, two
+// batches in flight per wave, XCD-contiguous tiles, last-split combine) with
+// the A operand now 16 activation rows. A lane streams its own 16 bytes of
+// the activation per step (row l & 15, K quarter l >> 4; L2-resident, shared
+// by every tile) beside the weight words, so there is no staging. The words
+// are dequantised to exact fp16 codes, the step products accumulate in fp32
+// per scale group (MFMA accumulator) and are scaled at each group's end.
+// Rows >= M read zeros. The waves' [16 x TN] results are added in LDS.
+// ---------------------------------------------------------------------------
+template <int CB, int GSHIFT>
+struct Gemv16Batch {
+    static constexpr int SB = kGemvBatch;
+    static constexpr int NG = SB >> GSHIFT;
+    static constexpr int SW = (CB + 1) / 2;
+    typename UIntVec<CB>::T w[SB];
+    u32x4 a[SB];
+    typename UIntVec<SW>::T s[NG];
+    __device__ __forceinline__ void load(const GemmParams& p, __amdgpu_buffer_rsrc_t rw,
+                                         __amdgpu_buffer_rsrc_t rs, const uint16_t* arow, bool arow_ok,
+                                         uint32_t w_off, uint32_t s_off, uint32_t step_bytes,
+                                         uint32_t grp_bytes, int step0, int last_step, int last_grp) {
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            // Steps past the split re-read its last step (in bounds) with a
+            // zero activation, so they add exactly 0.
+            const int st = min(step0 + j, last_step);
+            w[j] = buffer_load_words<CB>(rw, w_off, (uint32_t)st * step_bytes);
+            const u32x4 v = load16(arow + 32 * st);
+            a[j] = (arow_ok && step0 + j <= last_step) ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+        const int g0 = step0 >> p.gshift;
+#pragma unroll
+        for (int u = 0; u < NG; ++u) {
+            const uint32_t so = (uint32_t)min(g0 + u, last_grp) * grp_bytes;
+            if constexpr (CB == 1) s[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)so, 0);
+            else s[u] = buffer_load_words<SW>(rs, s_off, so);
+        }
+    }
+    __device__ __forceinline__ float scale(int u, int cb) const {
+        uint32_t d;
+        if constexpr (CB == 1) d = s[u];
+        else d = word_of<SW>(s[u], cb >> 1);
+        return h2f((uint16_t)((cb & 1) ? (d >> 16) : d));
+    }
+};
+
+template <int CB, int GSHIFT, bool MULTI>
+__global__ __launch_bounds__(kGemvThreads) void w4a16_gemv16_kernel(GemmParams p) {
+    constexpr int SB = kGemvBatch;
+    constexpr int TN = 16 * CB;
+    constexpr int SPG = 1 << GSHIFT;   // steps per group inside a batch (GSHIFT <= log2 SB)
+    __shared__ float s_red[kGemvWaves][16][TN + 1];
+    __shared__ uint32_t s_last;
+
+    int b = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
+    const int tile = b % p.n_tiles;
+    const int split = b / p.n_tiles;
+
+    const int steps = p.K / 32;
+    const int sps = p.kp_per_split / 4;
+    const int k0 = split * sps;
+    const int nst = min(sps, steps - k0);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15;
+    const int kq = lane >> 4;
+    const int n0 = tile * TN;
+    const int col0 = n0 + CB * c;
+
+    const int per_wave = sps / kGemvWaves;     // whole batches
+    const int s0 = wave * per_wave;
+    const int s1 = min(s0 + per_wave, nst);
+    const int last = k0 + nst - 1;
+    const int n_grp = p.K / p.group_size;
+    const __amdgpu_buffer_rsrc_t rw = make_buffer_rsrc(p.w, (uint32_t)(p.K / 8) * p.N * 4u);
+    const __amdgpu_buffer_rsrc_t rs = make_buffer_rsrc(p.scale, (uint32_t)n_grp * p.N * 2u);
+    const uint32_t w_off = ((uint32_t)kq * p.N + col0) * 4u;
+    const uint32_t s_off = (uint32_t)col0 * 2u;
+    const uint32_t step_bytes = (uint32_t)p.N * 16u;
+    const uint32_t grp_bytes = (uint32_t)p.N * 2u;
+    const bool arow_ok = c < p.M;
+    const uint16_t* arow = p.act + (long)min(c, p.M - 1) * p.K + 8 * kq;
+
+    Gemv16Batch<CB, GSHIFT> ba, bb;
+    ba.load(p, rw, rs, arow, arow_ok, w_off, s_off, step_bytes, grp_bytes, k0 + s0, last, n_grp - 1);
+    if constexpr (MULTI)
+        bb.load(p, rw, rs, arow, arow_ok, w_off, s_off, step_bytes, grp_bytes, k0 + s0 + SB, last,
+                n_grp - 1);
+
+    f32x4 acc[CB], cg[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        cg[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // Batches start on multiples of SB steps and groups span SPG steps
+    // (or the whole batch), so group ends fall at fixed batch offsets; a
+    // batch's steps past the split carry zero activations.
+    auto consume = [&](const Gemv16Batch<CB, GSHIFT>& bt) {
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            const u32x4 a = bt.a[j];
+            u32x4 r;
+            r[0] = perm_b32(a[2], a[0], 0x05040100u);   // a0 a4
+            r[1] = perm_b32(a[2], a[0], 0x07060302u);   // a1 a5
+            r[2] = perm_b32(a[3], a[1], 0x05040100u);   // a2 a6
+            r[3] = perm_b32(a[3], a[1], 0x07060302u);   // a3 a7
+            const f16x8 aop = __builtin_bit_cast(f16x8, r);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                f16x2 wp[4];
+                i4x8_to_f16_pairs(word_of<CB>(bt.w[j], cb), wp);
+                f16x8 bop;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bop[2 * i] = wp[i][0];
+                    bop[2 * i + 1] = wp[i][1];
+                }
+                cg[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, cg[cb], 0, 0, 0);
+            }
+            if ((j % SPG) == SPG - 1) {   // end of a group (or of the batch when groups are longer)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const float scv = bt.scale(j >> GSHIFT, cb);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[cb][i] = fmaf(scv, cg[cb][i], acc[cb][i]);
+                    cg[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+        }
+    };
+    if constexpr (!MULTI) {
+        if (s0 < s1) consume(ba);
+    } else if (s0 < s1) {
+        for (int b0 = s0;; b0 += 2 * SB) {
+            consume(ba);
+            if (b0 + SB >= s1) break;
+            ba.load(p, rw, rs, arow, arow_ok, w_off, s_off, step_bytes, grp_bytes, k0 + b0 + 2 * SB,
+                    last, n_grp - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(bb);
+            if (b0 + 2 * SB >= s1) break;
+            bb.load(p, rw, rs, arow, arow_ok, w_off, s_off, step_bytes, grp_bytes, k0 + b0 + 3 * SB,
+                    last, n_grp - 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // C layout: lane (c, kq) holds rows 4kq..4kq+3 of MFMA cb's columns
+    // (tile column CB * c + cb).
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_red[wave][4 * kq + i][CB * c + cb] = acc[cb][i];
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int row = t / TN, col = t % TN;   // 16 * TN <= kGemvThreads outputs, one per thread
+    float v = 0.0f;
+    const bool mine = t < 16 * TN && row < p.M;
+    if (mine) {
+#pragma unroll
+        for (int w = 0; w < kGemvWaves; ++w) v += s_red[w][row][col];
+    }
+    if (p.splits == 1) {
+        if (mine) store_out(p, row, n0 + col, v);
+        return;
+    }
+    if (mine) publish_store(&p.part[((long)split * p.M + row) * p.N + n0 + col], v);
+    publish_wait();
+    __syncthreads();
+    if (t == 0) s_last = arrive_last(&p.counters[tile], (uint32_t)p.splits) ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u) return;
+    if (mine)
+        store_out(p, row, n0 + col,
+                  sum_splits(p.part + (long)row * p.N + n0 + col, (long)p.M * p.N, p.splits));
+    if (t == 0) p.counters[tile] = 0u;
+}
+
+template <int CB, bool MULTI>
+static void launch_gemv16_cb(const GemmParams& p, int grid, hipStream_t stream) {
+    const dim3 g(grid), blk(kGemvThreads);
+    switch (min(p.gshift, 3)) {
+        case 0: hipLaunchKernelGGL((w4a16_gemv16_kernel<CB, 0, MULTI>), g, blk, 0, stream, p); break;
+        case 1: hipLaunchKernelGGL((w4a16_gemv16_kernel<CB, 1, MULTI>), g, blk, 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((w4a16_gemv16_kernel<CB, 2, MULTI>), g, blk, 0, stream, p); break;
+        default: hipLaunchKernelGGL((w4a16_gemv16_kernel<CB, 3, MULTI>), g, blk, 0, stream, p); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // M >= 2 on the matrix cores (N % 64 == 0, group_size a power of two >= 32).
 //
 // A workgroup of 4 waves computes a tile of TM = 16 * RT rows by 64 columns
@@ -706,14 +900,35 @@ __global__ __launch_bounds__(kMmaThreads) void w4a16_gemm_mfma_kernel(GemmParams
     if (threadIdx.x == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
+    // Last split: add the partials in split order. The loads of two splits
+    // for all of this thread's outputs are issued together, so the combine
+    // costs one memory round trip per two splits.
+    constexpr int NO = RT * 4;
+    float tot[NO];
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
+    for (int o = 0; o < NO; ++o) tot[o] = 0.0f;
+    for (int s0 = 0; s0 < p.splits; s0 += 2) {
+        float v[2][NO];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = out_index(r, i);
-            if (m < p.M)
-                store_out(p, m, n, sum_splits(p.part + (long)m * p.N + n, (long)p.M * p.N, p.splits));
+        for (int u = 0; u < 2; ++u) {
+            const long sp = min(s0 + u, p.splits - 1);
+#pragma unroll
+            for (int o = 0; o < NO; ++o) {
+                const int m = min(out_index(o >> 2, o & 3), p.M - 1);
+                v[u][o] = publish_load(&p.part[(sp * p.M + m) * p.N + n]);
+            }
         }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int o = 0; o < NO; ++o)
+                if (s0 + u < p.splits) tot[o] += v[u][o];
+    }
+#pragma unroll
+    for (int o = 0; o < NO; ++o) {
+        const int m = out_index(o >> 2, o & 3);
+        if (m < p.M) store_out(p, m, n, tot[o]);
+    }
     if (threadIdx.x == 0) p.counters[counter] = 0u;
 }
 
@@ -914,6 +1129,34 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
             return pl;
         }
     }
+    if (M >= 2 && M <= 16 && N % 32 == 0 && pow2_group && K % 32 == 0 &&
+        (long)(K / 8) * N * 4 < (1L << 31)) {
+        // Matrix-core GEMV over 16 rows: the single-row plan with 32-column tiles.
+        const int cb = 2;
+        const int sb = kGemvBatch * kGemvWaves;
+        const int steps = K / 32;
+        const int tiles = N / (16 * cb);
+        const long target = (long)LLMIK_GEMV_WGS_PER_CU * device_cu_count();
+        long want = (target + tiles - 1) / tiles;
+        const long max_splits = (steps + sb - 1) / sb;
+        if (want > max_splits) want = max_splits;
+        if (tiles > kMaxCounters) want = 1;
+        if (want < 1) want = 1;
+        int sps = (int)((steps + want - 1) / want);
+        sps = (sps + sb - 1) / sb * sb;
+        pl.kind = 4;
+        pl.cols_per_lane = cb;
+        pl.tile_n = 16 * cb;
+        pl.tile_m = 16;
+        pl.n_tiles = tiles;
+        pl.m_tiles = 1;
+        pl.kp_per_split = 4 * sps;
+        pl.splits = (steps + sps - 1) / sps;
+        pl.off_part = kCounterBytes;
+        pl.workspace_bytes =
+            (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
+        return pl;
+    }
     if (M >= 2 && N % 64 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31)) {
         // Matrix-core GEMM: tiles of 16 * rt rows by 64 columns.
         int rt = 1;
@@ -1001,6 +1244,10 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
             case 2: launch_gemv_cb<2>(p, grid, sps, stream); break;
             default: launch_gemv_cb<1>(p, grid, sps, stream); break;
         }
+    } else if (pl.kind == 4) {
+        const int grid = pl.n_tiles * pl.splits;
+        if (pl.kp_per_split / 4 / kGemvWaves > kGemvBatch) launch_gemv16_cb<2, true>(p, grid, stream);
+        else launch_gemv16_cb<2, false>(p, grid, stream);
     } else if (pl.kind == 3) {
         const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kMmaThreads);
         switch (pl.tile_m) {

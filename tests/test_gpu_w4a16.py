@@ -74,7 +74,10 @@ def test_llama_shapes(llmik, cuda, M, K, N):
                                       # M >= 2 matrix-core GEMM: row tiles 1/2/4/8, partial and
                                       # several m tiles, one-step K, groups 32..256
                                       (2, 1024, 128, 32), (17, 512, 192, 64), (33, 2048, 64, 256),
-                                      (100, 384, 128, 128), (200, 256, 64, 32), (7, 32, 64, 32)])
+                                      (100, 384, 128, 128), (200, 256, 64, 32), (7, 32, 64, 32),
+                                      # 2 <= M <= 16 matrix-core GEMV: 32-column tiles, splits,
+                                      # a K range that ends inside a batch
+                                      (3, 4096, 96, 128), (16, 1056, 32, 32), (9, 7168, 64, 512)])
 def test_odd_shapes(llmik, cuda, M, K, N, gs):
     _check(llmik, cuda, M, K, N, gs, seed=M * 7 + K)
 
