@@ -19,61 +19,144 @@
 namespace llmik {
 
 constexpr int kWriterThreads = 256;   // 16 token rows of 16 lanes
+constexpr int kTokensPerRow = 2;      // per-token writer: tokens per 16-lane row
 
-// One DPP row (16 lanes) per token: lane c owns channels 8c..8c+7.
+// Per token: one DPP row (16 lanes) per token, lane c owns channels
+// 8c..8c+7. A workgroup covers 16 * kTokensPerRow consecutive tokens; the
+// row's loads for all its tokens are issued before any is used (token
+// i * 16 + row of the workgroup's block, so each i reads 4 KiB contiguous).
 template <int QMAX, bool PACK4>
 __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, uint16_t* __restrict__ scale,
     long rows) {
-    const long row = (long)blockIdx.x * (kWriterThreads / 16) + (threadIdx.x >> 4);
+    const long blk = (long)blockIdx.x * (16 * kTokensPerRow);
+    const int rr = threadIdx.x >> 4;
     const int c = threadIdx.x & 15;
-    // Rows past the end still take part in the DPP reduction (on a clamped,
-    // in-bounds row) but store nothing.
-    const long r = row < rows ? row : rows - 1;
-
-    float xf[8];
-    f16x8_to_f32(load16(x + r * 128 + 8 * c), xf);
-    float amax = 0.0f;
+    u32x4 raw[kTokensPerRow];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xf[e]));
-    amax = row16_max(amax);
-
-    const float s = fmaxf(amax / (float)QMAX, 1.0e-8f);
-    const float rcp = 1.0f / s;
-    int code[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        float v = quant_round(xf[e], s, rcp);
-        v = fminf(fmaxf(v, -(float)QMAX), (float)QMAX);
-        code[e] = (int)v;
+    for (int i = 0; i < kTokensPerRow; ++i) {
+        // Rows past the end still take part in the DPP reduction (on a
+        // clamped, in-bounds row) but store nothing.
+        const long row = min(blk + 16 * i + rr, rows - 1);
+        raw[i] = stream16(x + row * 128 + 8 * c);
     }
-    if (row >= rows) return;
-
-    if constexpr (PACK4) {
-        uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) w |= (uint32_t)(code[e] & 0xF) << (4 * e);
-        *reinterpret_cast<uint32_t*>(q + row * 64 + 4 * c) = w;
-    } else {
-        u32x2 w;
-        w[0] = (uint32_t)(code[0] & 0xFF) | ((uint32_t)(code[1] & 0xFF) << 8) |
-               ((uint32_t)(code[2] & 0xFF) << 16) | ((uint32_t)(code[3] & 0xFF) << 24);
-        w[1] = (uint32_t)(code[4] & 0xFF) | ((uint32_t)(code[5] & 0xFF) << 8) |
-               ((uint32_t)(code[6] & 0xFF) << 16) | ((uint32_t)(code[7] & 0xFF) << 24);
-        *reinterpret_cast<u32x2*>(q + row * 128 + 8 * c) = w;
+    for (int i = 0; i < kTokensPerRow; ++i) {
+        const long row = blk + 16 * i + rr;
+        float xf[8];
+        f16x8_to_f32(raw[i], xf);
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xf[e]));
+        amax = row16_max(amax);
+
+        const float sc = fmaxf(amax / (float)QMAX, 1.0e-8f);
+        const float rcp = 1.0f / sc;
+        int code[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = quant_round(xf[e], sc, rcp);
+            v = fminf(fmaxf(v, -(float)QMAX), (float)QMAX);
+            code[e] = (int)v;
+        }
+        if (row < rows) {
+            if constexpr (PACK4) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w |= (uint32_t)(code[e] & 0xF) << (4 * e);
+                __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(q + row * 64 + 4 * c));
+            } else {
+                u32x2 w;
+                w[0] = (uint32_t)(code[0] & 0xFF) | ((uint32_t)(code[1] & 0xFF) << 8) |
+                       ((uint32_t)(code[2] & 0xFF) << 16) | ((uint32_t)(code[3] & 0xFF) << 24);
+                w[1] = (uint32_t)(code[4] & 0xFF) | ((uint32_t)(code[5] & 0xFF) << 8) |
+                       ((uint32_t)(code[6] & 0xFF) << 16) | ((uint32_t)(code[7] & 0xFF) << 24);
+                __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(q + row * 128 + 8 * c));
+            }
+            if (c == 0) scale[row] = f2h_bits(sc);
+        }
     }
-    if (c == 0) scale[row] = f2h_bits(s);
 }
 
-// One workgroup per (batch, kv_head, group). 16 rows of 16 lanes: row r
-// walks the group's tokens r, r+16, ...; lane c owns channels 8c..8c+7.
-// Pass 1 takes the per-channel absmax (rows merged in LDS), pass 2
-// re-reads the (cache-resident) group and writes packed codes.
+// K per channel, group-wise: one workgroup per (batch, kv_head, group). 16
+// rows of 16 lanes: row r holds the group's tokens r, r+16, ... (at most
+// TPR of them, group_size <= 16 * TPR) in registers; lane c owns channels
+// 8c..8c+7. The per-channel absmax is merged across rows in LDS, then the
+// codes are formed from the registers: the input is read once.
+template <int TPR>
 __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, uint16_t* __restrict__ scale,
     int seqlen, int group_size, int n_groups) {
     const int g = blockIdx.x;
     const long bh = blockIdx.y;   // batch * n_kv_heads + kv_head
+    const int row = threadIdx.x >> 4;
+    const int c = threadIdx.x & 15;
+    const int t_start = g * group_size;
+    const int t_end = min(t_start + group_size, seqlen);
+    const long base = bh * seqlen;
+
+    u32x4 raw[TPR];
+#pragma unroll
+    for (int i = 0; i < TPR; ++i) {
+        const int t = min(t_start + row + 16 * i, t_end - 1);   // in bounds; duplicates do not move the max
+        raw[i] = stream16(x + (base + t) * 128 + 8 * c);
+    }
+    float amax[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TPR; ++i) {
+        float xf[8];
+        f16x8_to_f32(raw[i], xf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax[e] = fmaxf(amax[e], fabsf(xf[e]));
+    }
+
+    __shared__ float s_max[16][128];
+    __shared__ float s_scale[128];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_max[row][8 * c + e] = amax[e];
+    __syncthreads();
+    if (threadIdx.x < 128) {
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, s_max[r][threadIdx.x]);
+        const float sc = fmaxf(m / 7.0f, 1.0e-8f);
+        s_scale[threadIdx.x] = sc;
+        scale[(bh * n_groups + g) * 128 + threadIdx.x] = f2h_bits(sc);
+    }
+    __syncthreads();
+
+    float sv[8], rcp[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        sv[e] = s_scale[8 * c + e];
+        rcp[e] = 1.0f / sv[e];
+    }
+#pragma unroll
+    for (int i = 0; i < TPR; ++i) {
+        const int t = t_start + row + 16 * i;
+        float xf[8];
+        f16x8_to_f32(raw[i], xf);
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = quant_round(xf[e], sv[e], rcp[e]);
+            v = fminf(fmaxf(v, -7.0f), 7.0f);
+            w |= (uint32_t)((int)v & 0xF) << (4 * e);
+        }
+        if (t < t_end)
+            __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(q + (base + t) * 64 + 4 * c));
+    }
+}
+
+// Group sizes beyond 16 * 8 tokens: the group is walked twice (max, then
+// codes); the second pass re-reads it from the caches.
+__global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_large_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, uint16_t* __restrict__ scale,
+    int seqlen, int group_size, int n_groups) {
+    const int g = blockIdx.x;
+    const long bh = blockIdx.y;
     const int row = threadIdx.x >> 4;
     const int c = threadIdx.x & 15;
     const int t_start = g * group_size;
@@ -99,17 +182,17 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
         float m = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) m = fmaxf(m, s_max[r][threadIdx.x]);
-        const float s = fmaxf(m / 7.0f, 1.0e-8f);
-        s_scale[threadIdx.x] = s;
-        scale[(bh * n_groups + g) * 128 + threadIdx.x] = f2h_bits(s);
+        const float sc = fmaxf(m / 7.0f, 1.0e-8f);
+        s_scale[threadIdx.x] = sc;
+        scale[(bh * n_groups + g) * 128 + threadIdx.x] = f2h_bits(sc);
     }
     __syncthreads();
 
-    float s[8], rcp[8];
+    float sv[8], rcp[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        s[e] = s_scale[8 * c + e];
-        rcp[e] = 1.0f / s[e];
+        sv[e] = s_scale[8 * c + e];
+        rcp[e] = 1.0f / sv[e];
     }
     for (int t = t_start + row; t < t_end; t += 16) {
         float xf[8];
@@ -117,7 +200,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
         uint32_t w = 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            float v = quant_round(xf[e], s[e], rcp[e]);
+            float v = quant_round(xf[e], sv[e], rcp[e]);
             v = fminf(fmaxf(v, -7.0f), 7.0f);
             w |= (uint32_t)((int)v & 0xF) << (4 * e);
         }
@@ -128,7 +211,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
 int launch_quantize_per_token(const void* x, void* q, void* scale, long rows, int qmax,
                               bool pack4, hipStream_t stream) {
     if (rows == 0) return LLMIK_OK;
-    const long rows_per_wg = kWriterThreads / 16;
+    const long rows_per_wg = 16 * kTokensPerRow;
     const long grid = (rows + rows_per_wg - 1) / rows_per_wg;
     if (grid > 0x7FFFFFFFL) return set_error(LLMIK_ERR_UNSUPPORTED, "too many token rows");
     auto xp = static_cast<const uint16_t*>(x);
@@ -153,10 +236,20 @@ int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int ba
     const int n_groups = (seqlen + group_size - 1) / group_size;
     const long bh = (long)batch * n_kv_heads;
     if (bh > 65535L) return set_error(LLMIK_ERR_UNSUPPORTED, "batch * n_kv_heads exceeds 65535");
-    hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel, dim3(n_groups, (unsigned)bh),
-                       dim3(kWriterThreads), 0, stream, static_cast<const uint16_t*>(x),
-                       static_cast<int8_t*>(q), static_cast<uint16_t*>(scale), seqlen,
-                       group_size, n_groups);
+    const dim3 grid(n_groups, (unsigned)bh), blk(kWriterThreads);
+    auto xp = static_cast<const uint16_t*>(x);
+    auto qp = static_cast<int8_t*>(q);
+    auto sp = static_cast<uint16_t*>(scale);
+    if (group_size <= 16)
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<1>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+    else if (group_size <= 32)
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<2>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+    else if (group_size <= 64)
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<4>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+    else if (group_size <= 128)
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<8>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+    else
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_large_kernel, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
     return check_launch();
 }
 

@@ -57,6 +57,19 @@ def test_int4_v_per_token_bit_exact(llmik, cuda, shape):
 @pytest.mark.parametrize("shape", SHAPES + [(2, 8, 100, 128), (1, 2, 37, 128)])
 @pytest.mark.parametrize("gs", [32, 128, 64])
 def test_int4_k_groupwise_bit_exact(llmik, cuda, shape, gs):
+    _check_k_groupwise(llmik, cuda, shape, gs)
+
+
+# Group sizes that take the other register-resident widths (<= 16 tokens,
+# a group that does not fill its rows) and the two-pass path (> 128).
+@pytest.mark.parametrize("shape,gs", [((1, 8, 100, 128), 8), ((2, 4, 70, 128), 16),
+                                      ((1, 8, 300, 128), 96), ((2, 8, 600, 128), 256),
+                                      ((1, 2, 37, 128), 512)])
+def test_int4_k_groupwise_other_group_sizes(llmik, cuda, shape, gs):
+    _check_k_groupwise(llmik, cuda, shape, gs)
+
+
+def _check_k_groupwise(llmik, cuda, shape, gs):
     x = _special(kv_with_outliers(shape, seed=shape[2] + gs).astype(np.float16))
     q, s = llmik.quantize_k_per_channel_groupwise_int4(_dev(x, cuda), gs)
     rq, rs = kq.quantize_per_channel_groupwise(x.astype(np.float32), 4, gs)
