@@ -17,6 +17,8 @@
 #include "device_common.hpp"
 #include "llmik_internal.hpp"
 
+#include <cstdlib>
+
 namespace llmik {
 
 constexpr int kGemmThreads = 256;   // 4 waves share one column tile
@@ -33,6 +35,8 @@ struct GemmParams {
     int splits, kp_per_split, n_tiles;
     int f32_out;
     int gshift;          // log2(group_size / 32) on the matrix-core GEMV
+    int nw;              // streaming GEMV: waves per workgroup
+    int wave_steps;      // streaming GEMV: 32-K steps per wave
 };
 
 // Eight int4 codes of one word -> four fp16 pairs, exact. Pair j holds the
@@ -508,6 +512,257 @@ static void launch_gemv_cb(const GemmParams& p, int grid, int sps, hipStream_t s
             case 3: launch_gemv_cb_stage<CB, 3, false>(p, grid, lds, stream); break;
             default: launch_gemv_cb_stage<CB, kGemvMaxStage, false>(p, grid, lds, stream); break;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 1 <= M <= 16, N % 64 == 0, group_size a power of two >= 32: streaming
+// matrix-core GEMV (plan kind 5; the default for the decode shapes).
+//
+// A workgroup owns a 64-column tile and one K split; its nw (8..16) waves
+// take consecutive ranges of wave_steps 32-K steps. Lane (kq, c) owns tile
+// columns 4c..4c+3: per step it loads the 16-byte word quad of packed row
+// 4*step + kq and, beside it, its own 16-byte fragment of activation row c
+// (K offset 32*step + 8*kq; rows >= M read as zero). Weights and activation
+// arrive together, so a step's arithmetic needs nothing staged and no
+// barrier (an activation staged per workgroup would queue behind the
+// weight stream of the whole chip before the first product could start).
+// Every load of a batch is issued before any arithmetic waits on one; at
+// most two batches are in flight per wave.
+//
+// Words enter the MFMA biased: with u = code + 8, 0x6400 | u is the fp16
+// value 1024 + u and 0x6400 | u << 4 is 1024 + 16u, in the pair order
+// (i0,i4), (i1,i5), (i2,i6), (i3,i7). The activation fragment is permuted
+// to that order with the odd offsets divided by 16 (exact), so a product
+// carries a bias of 1032 a (even offsets) or 72 a (odd offsets). One more
+// MFMA per step, of the same activation against the constant operand
+// (-1032, -1032, -1152, -1152, ...), accumulates minus that bias beside the
+// four column accumulators; the scale is applied once per scale group:
+//   acc[n] += scale[g][n] * (C_g[n] + Cbias_g).
+// The waves' [MR x 64] partials are added in LDS in a fixed order.
+// ---------------------------------------------------------------------------
+constexpr int kStreamMaxWaves = 16;
+constexpr int kStreamTile = 64;
+
+template <int SB, int GSHIFT>
+struct StreamBatch {
+    static constexpr int NG = ((SB >> GSHIFT) > 0) ? (SB >> GSHIFT) : 1;
+    u32x4 w[SB];
+    u32x4 a[SB];
+    u32x2 s[NG];
+};
+
+// NB > 0: the wave's NB batches are all issued up front. NB == 0: a loop
+// over wave_steps / SB (even, >= 4) batches with two in flight.
+template <int MR, int SB, int GSHIFT, int NB>
+__global__ __launch_bounds__(kStreamMaxWaves * kWave) void w4a16_gemv_stream_kernel(GemmParams p) {
+    constexpr int SPG = 1 << GSHIFT;   // steps per scale flush (a group, or the batch)
+    constexpr int TN = kStreamTile;
+    constexpr int NRED = kStreamMaxWaves / 2;
+    __shared__ float s_red[NRED][MR][TN + 1];
+    __shared__ uint32_t s_last;
+
+    const int b = blockIdx.x;
+    const int tile = b % p.n_tiles;
+    const int split = b / p.n_tiles;
+    const int steps = p.K / 32;
+    const int sps = p.kp_per_split / 4;
+    const int k0 = split * sps;
+    const int nst = min(sps, steps - k0);
+    const int nw = p.nw;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15;
+    const int kq = lane >> 4;
+    const int n0 = tile * TN;
+    const int col0 = n0 + 4 * c;
+    const int ws0 = k0 + wave * p.wave_steps;                  // the wave's first step
+    const int ws1 = min(ws0 + p.wave_steps, k0 + nst);         // one past its last
+    // Loads of steps outside [ws0, ws1) re-read a step of the split (in
+    // bounds, cached) and meet a zero activation, so they add exactly 0.
+    const int lastvalid = (ws1 > ws0) ? ws1 - 1 : k0 + nst - 1;
+    const int n_grp = p.K / p.group_size;
+
+    const __amdgpu_buffer_rsrc_t rw = make_buffer_rsrc(p.w, (uint32_t)(p.K / 8) * p.N * 4u);
+    const __amdgpu_buffer_rsrc_t ra = make_buffer_rsrc(p.act, (uint32_t)p.M * p.K * 2u);
+    const __amdgpu_buffer_rsrc_t rs = make_buffer_rsrc(p.scale, (uint32_t)n_grp * p.N * 2u);
+    const uint32_t w_off = ((uint32_t)kq * p.N + col0) * 4u;
+    const uint32_t a_off = ((uint32_t)min(c, p.M - 1) * p.K + 8u * kq) * 2u;
+    const uint32_t s_off = (uint32_t)col0 * 2u;
+    const uint32_t step_bytes = (uint32_t)p.N * 16u;
+    const uint32_t grp_bytes = (uint32_t)p.N * 2u;
+    const bool row_ok = c < p.M;
+
+    using Batch = StreamBatch<SB, GSHIFT>;
+    auto load_batch = [&](Batch& bt, int sb0) {
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            const uint32_t st = (uint32_t)min(sb0 + j, lastvalid);
+            bt.w[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)w_off, (int)(st * step_bytes), 2);
+            bt.a[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)a_off, (int)(st * 64u), 0);
+        }
+        const int g0 = min(sb0, lastvalid) >> p.gshift;
+#pragma unroll
+        for (int u = 0; u < Batch::NG; ++u) {
+            const uint32_t so = (uint32_t)min(g0 + u, n_grp - 1) * grp_bytes;
+            bt.s[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)s_off, (int)so, 0);
+        }
+    };
+
+    // The masks and the exponent bits live in VGPRs so that each
+    // (word & mask) | bias is a single three-operand bit op.
+    const uint32_t m_lo = vgpr_const(0x000F000Fu);
+    const uint32_t m_hi = vgpr_const(0x00F000F0u);
+    const uint32_t bias = vgpr_const(0x64006400u);
+    // fp16 -1032 = 0xE408, -1152 = 0xE480
+    const f16x8 bias_op =
+        __builtin_bit_cast(f16x8, make_u32x4(0xE408E408u, 0xE480E480u, 0xE408E408u, 0xE480E480u));
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    f32x4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto consume = [&](const Batch& bt, int sb0) {
+        f32x4 cg[4], cb4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cg[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            u32x4 a = bt.a[j];
+            if (!row_ok || sb0 + j >= ws1) a = u32x4{0u, 0u, 0u, 0u};
+            const f16x2 odd0 = as_f16x2(perm_b32(a[2], a[0], 0x07060302u)) * sixteenth;   // a1 a5
+            const f16x2 odd1 = as_f16x2(perm_b32(a[3], a[1], 0x07060302u)) * sixteenth;   // a3 a7
+            const f16x8 aop = __builtin_bit_cast(f16x8, make_u32x4(
+                perm_b32(a[2], a[0], 0x05040100u), __builtin_bit_cast(uint32_t, odd0),     // a0 a4
+                perm_b32(a[3], a[1], 0x05040100u), __builtin_bit_cast(uint32_t, odd1)));   // a2 a6
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t wv = bt.w[j][q] ^ 0x88888888u;
+                const uint32_t w8 = wv >> 8;
+                const u32x4 braw = make_u32x4((wv & m_lo) | bias, (wv & m_hi) | bias,
+                                              (w8 & m_lo) | bias, (w8 & m_hi) | bias);
+                cg[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, __builtin_bit_cast(f16x8, braw),
+                                                                cg[q], 0, 0, 0);
+            }
+            cb4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bias_op, cb4, 0, 0, 0);
+            if ((j & (SPG - 1)) == SPG - 1) {
+                const u32x2 sv = bt.s[j >> GSHIFT];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t d = sv[q >> 1];
+                    const float scv = h2f((uint16_t)((q & 1) ? (d >> 16) : d));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[q][i] = fmaf(scv, cg[q][i] + cb4[i], acc[q][i]);
+                    cg[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+                cb4 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    };
+
+    if constexpr (NB > 0) {
+        Batch bt[NB];
+#pragma unroll
+        for (int ib = 0; ib < NB; ++ib) load_batch(bt[ib], ws0 + ib * SB);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ib = 0; ib < NB; ++ib) consume(bt[ib], ws0 + ib * SB);
+    } else {
+        const int nbw = p.wave_steps / SB;   // even, >= 4
+        Batch b0, b1;
+        load_batch(b0, ws0);
+        load_batch(b1, ws0 + SB);
+        __builtin_amdgcn_sched_barrier(0);
+        int i = 0;
+        for (; i + 2 < nbw; i += 2) {
+            consume(b0, ws0 + i * SB);
+            load_batch(b0, ws0 + (i + 2) * SB);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(b1, ws0 + (i + 1) * SB);
+            load_batch(b1, ws0 + (i + 3) * SB);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        consume(b0, ws0 + i * SB);
+        consume(b1, ws0 + (i + 1) * SB);
+    }
+
+    // C layout: lane (c, kq) holds rows 4kq + i of tile columns 4c + q.
+    // Waves >= NRED hand their partial to wave - NRED, which adds it; the
+    // NRED slots are then summed in order.
+    auto put = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * kq + i;
+            if (row < MR) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) s_red[slot][row][4 * c + q] = acc[q][i];
+            }
+        }
+    };
+    if (wave >= NRED) put(wave - NRED);
+    __syncthreads();
+    if (wave < NRED) {
+        if (wave + NRED < nw) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 4 * kq + i;
+                if (row < MR) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[q][i] += s_red[wave][row][4 * c + q];
+                }
+            }
+        }
+        put(wave);
+    }
+    __syncthreads();
+    // Outputs of the tile (min(M, MR) rows x 64 columns), strided over the
+    // workgroup's nw * 64 threads.
+    const int t = threadIdx.x;
+    const int nthreads = nw * kWave;
+    const int nout = min(p.M, MR) * TN;
+    const int nslots = min(nw, NRED);
+    auto tile_sum = [&](int o) {
+        float v = 0.0f;
+        for (int w = 0; w < nslots; ++w) v += s_red[w][o / TN][o % TN];
+        return v;
+    };
+    if (p.splits == 1) {
+        for (int o = t; o < nout; o += nthreads) store_out(p, o / TN, n0 + o % TN, tile_sum(o));
+        return;
+    }
+    for (int o = t; o < nout; o += nthreads)
+        publish_store(&p.part[((long)split * p.M + o / TN) * p.N + n0 + o % TN], tile_sum(o));
+    publish_wait();
+    __syncthreads();
+    if (t == 0) s_last = arrive_last(&p.counters[tile], (uint32_t)p.splits) ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u) return;
+    for (int o = t; o < nout; o += nthreads) {
+        const int row = o / TN, col = o % TN;
+        store_out(p, row, n0 + col,
+                  sum_splits(p.part + (long)row * p.N + n0 + col, (long)p.M * p.N, p.splits));
+    }
+    if (t == 0) p.counters[tile] = 0u;
+}
+
+template <int MR, int SB, int NB>
+static void launch_stream_sb(const GemmParams& p, int grid, hipStream_t stream) {
+    const dim3 g(grid), blk(p.nw * kWave);
+    constexpr int MAXG = (SB >= 4) ? 2 : 1;   // log2 SB
+    switch (min(p.gshift, MAXG)) {
+        case 0: hipLaunchKernelGGL((w4a16_gemv_stream_kernel<MR, SB, 0, NB>), g, blk, 0, stream, p); break;
+        case 1: hipLaunchKernelGGL((w4a16_gemv_stream_kernel<MR, SB, 1, NB>), g, blk, 0, stream, p); break;
+        default: hipLaunchKernelGGL((w4a16_gemv_stream_kernel<MR, SB, MAXG, NB>), g, blk, 0, stream, p); break;
+    }
+}
+
+template <int MR>
+static void launch_stream(const GemmParams& p, int grid, hipStream_t stream) {
+    switch (p.wave_steps) {
+        case 2: launch_stream_sb<MR, 2, 1>(p, grid, stream); break;
+        case 4: launch_stream_sb<MR, 4, 1>(p, grid, stream); break;
+        case 8: launch_stream_sb<MR, 4, 2>(p, grid, stream); break;
+        default: launch_stream_sb<MR, 4, 0>(p, grid, stream); break;
     }
 }
 
@@ -1096,9 +1351,63 @@ __global__ __launch_bounds__(256) void w4a16_dequantize_kernel(const uint32_t* _
 // Host side
 // ---------------------------------------------------------------------------
 
+// Streaming GEMV selection: "1" forces it wherever the shape allows, "0"
+// disables it; unset, it serves weights of at least kStreamMinWeightBytes
+// (below that the single-row / 16-row GEMVs with 32-column tiles have less
+// fixed cost per call).
+constexpr long kStreamMinWeightBytes = 16L << 20;
+
+static int stream_override() {
+    const char* e = getenv("LLMIK_W4A16_STREAM");
+    if (e == nullptr || *e == '\0') return -1;
+    return (*e == '0') ? 0 : 1;
+}
+
 GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     GemmPlan pl{};
     const bool pow2_group = group_size >= 32 && (group_size & (group_size - 1)) == 0;
+    const int stream_mode = stream_override();
+    const bool stream_size_ok = (long)K * N / 2 >= kStreamMinWeightBytes;
+    if (M >= 1 && M <= 16 && N % 64 == 0 && pow2_group && K % 32 == 0 &&
+        (long)(K / 8) * N * 4 < (1L << 31) && (long)M * K * 2 < (1L << 31) &&
+        (stream_mode == 1 || (stream_mode < 0 && stream_size_ok))) {
+        // Streaming GEMV: as many K splits as whole workgroups per CU allow
+        // (no second round of workgroups), then the wave count (8..16) and
+        // steps per wave that cover a split with the fewest idle steps.
+        const int steps = K / 32;
+        const int tiles = N / 64;
+        long want = (long)device_cu_count() / tiles;
+        if (want < 1 || tiles > kMaxCounters) want = 1;
+        if (want > steps / 2) want = steps / 2 > 0 ? steps / 2 : 1;
+        const int need = (int)((steps + want - 1) / want);
+        int best_nw = kStreamMaxWaves, best_ws = 0;
+        long best_waste = -1;
+        for (int nw = kStreamMaxWaves; nw >= kStreamMaxWaves / 2; --nw) {
+            int ws = (need + nw - 1) / nw;
+            ws = ws <= 2 ? 2 : ws <= 4 ? 4 : (ws + 7) / 8 * 8;
+            const long waste = (long)nw * ws - need;
+            if (best_waste < 0 || waste < best_waste) {
+                best_waste = waste;
+                best_nw = nw;
+                best_ws = ws;
+            }
+        }
+        const int sps = best_nw * best_ws;
+        pl.kind = 5;
+        pl.waves = best_nw;
+        pl.wave_steps = best_ws;
+        pl.cols_per_lane = 4;
+        pl.tile_n = kStreamTile;
+        pl.tile_m = 16;
+        pl.n_tiles = tiles;
+        pl.m_tiles = 1;
+        pl.kp_per_split = 4 * sps;
+        pl.splits = (steps + sps - 1) / sps;
+        pl.off_part = kCounterBytes;
+        pl.workspace_bytes = (pl.splits > 1)
+            ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
+        return pl;
+    }
     if (M == 1 && N % 16 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31)) {
         // Matrix-core GEMV: widest tile (16 * cb columns) that divides N.
         int cb = LLMIK_GEMV_CB;
@@ -1235,7 +1544,15 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
     p.f32_out = f32_out ? 1 : 0;
     p.gshift = 0;
     while ((32 << p.gshift) < group_size) ++p.gshift;
+    p.nw = pl.waves;
+    p.wave_steps = pl.wave_steps;
     dim3 block(kGemmThreads);
+    if (pl.kind == 5) {
+        const int grid = pl.n_tiles * pl.splits;
+        if (M == 1) launch_stream<1>(p, grid, stream);
+        else launch_stream<16>(p, grid, stream);
+        return check_launch();
+    }
     if (pl.kind == 2) {
         const int grid = pl.n_tiles * pl.splits;
         const int sps = pl.kp_per_split / 4;
