@@ -159,6 +159,39 @@ LLMIK_API llmik_status llmik_quantize_v_per_token_int4(
     const void* x, void* q, void* scale, int batch, int n_kv_heads, int seqlen, int head_dim,
     void* stream);
 
+/* ------------------------------------------------- in-place KV-cache writers
+ * The same quantisers writing into a preallocated cache at a token offset,
+ * so a growing cache is appended to in place instead of being rebuilt.
+ * Replaces: the torch.cat of freshly quantised chunks onto the whole packed
+ *   cache in Int4KIVICache.append_only / get_quantized_for_attention
+ *   (integration/kv_int4_cache.py:119-144,184-206), which calls the
+ *   writers above on each chunk; the quantiser arithmetic is theirs.
+ *   x           [batch, n_kv_heads, x_len, head_dim] fp16; tokens [0, n_tok)
+ *               of each (batch, kv_head) row are quantised
+ *   q_cache     [batch, n_kv_heads, cache_len, head_dim] int8 (INT8) or
+ *               [batch, n_kv_heads, cache_len, head_dim/2] packed int4
+ *   scale_cache [batch, n_kv_heads, cache_len] fp16 (per token) or
+ *               [batch, n_kv_heads, ceil(cache_len/group_size), head_dim]
+ *               fp16 (K per channel, group-wise)
+ * Token t is written to cache position offset + t (offset + n_tok <=
+ * cache_len); nothing else in the cache is touched. The codes and scales
+ * are bit-identical to the out-of-place writer applied to those tokens.
+ */
+LLMIK_API llmik_status llmik_quantize_per_token_int8_into(const void* x, int x_len, void* q_cache,
+                                                          void* scale_cache, int batch,
+                                                          int n_kv_heads, int n_tok, int head_dim,
+                                                          int cache_len, int offset, void* stream);
+LLMIK_API llmik_status llmik_quantize_v_per_token_int4_into(const void* x, int x_len, void* q_cache,
+                                                            void* scale_cache, int batch,
+                                                            int n_kv_heads, int n_tok, int head_dim,
+                                                            int cache_len, int offset, void* stream);
+/* offset must be a multiple of group_size: tokens [offset, offset + n_tok)
+ * form ceil(n_tok / group_size) groups, the last one possibly partial (its
+ * scale uses only its real tokens, as the out-of-place writer does). */
+LLMIK_API llmik_status llmik_quantize_k_per_channel_groupwise_int4_into(
+    const void* x, int x_len, void* q_cache, void* scale_cache, int batch, int n_kv_heads,
+    int n_tok, int head_dim, int cache_len, int offset, int group_size, void* stream);
+
 /* -------------------------------------------------------------------- W4A16
  * out[M, N] = act[M, K] @ dequant(W)[K, N], W[k, n] = q[k, n] * scale[k/g, n],
  * fp32 accumulation.

@@ -190,10 +190,9 @@ LLMIK_API llmik_status llmik_quantize_per_token_int8(const void* x, void* q, voi
     int st = check_writer(x, q, scale, batch, n_kv_heads, seqlen, head_dim);
     if (st != LLMIK_OK) return st;
     if (!aligned(q, 8)) return set_error(LLMIK_ERR_ALIGNMENT, "q must be 8-byte aligned");
-    return launch_quantize_per_token(x, q, scale, (long)batch * n_kv_heads * seqlen, 127, false,
-                                     as_stream(stream));
+    return launch_quantize_per_token(x, q, scale, batch * n_kv_heads, seqlen, seqlen, seqlen, 0,
+                                     127, false, as_stream(stream));
 }
-
 LLMIK_API llmik_status llmik_quantize_k_per_channel_groupwise_int4(const void* x, void* q,
                                                                    void* scale, int batch,
                                                                    int n_kv_heads, int seqlen,
@@ -202,17 +201,69 @@ LLMIK_API llmik_status llmik_quantize_k_per_channel_groupwise_int4(const void* x
     int st = check_writer(x, q, scale, batch, n_kv_heads, seqlen, head_dim);
     if (st != LLMIK_OK) return st;
     if (group_size <= 0) return invalid("group_size must be positive");
-    return launch_quantize_k_groupwise_int4(x, q, scale, batch, n_kv_heads, seqlen, group_size,
-                                            as_stream(stream));
+    const int n_groups = seqlen > 0 ? (seqlen + group_size - 1) / group_size : 0;
+    return launch_quantize_k_groupwise_int4(x, q, scale, batch * n_kv_heads, seqlen, seqlen,
+                                            seqlen, 0, n_groups, group_size, as_stream(stream));
 }
-
 LLMIK_API llmik_status llmik_quantize_v_per_token_int4(const void* x, void* q, void* scale,
                                                        int batch, int n_kv_heads, int seqlen,
                                                        int head_dim, void* stream) {
     int st = check_writer(x, q, scale, batch, n_kv_heads, seqlen, head_dim);
     if (st != LLMIK_OK) return st;
-    return launch_quantize_per_token(x, q, scale, (long)batch * n_kv_heads * seqlen, 7, true,
-                                     as_stream(stream));
+    return launch_quantize_per_token(x, q, scale, batch * n_kv_heads, seqlen, seqlen, seqlen, 0, 7,
+                                     true, as_stream(stream));
+}
+
+// ---- in-place (cache) writers ----------------------------------------------
+namespace {
+int check_into(const void* x, int x_len, const void* q, const void* scale, int batch,
+               int n_kv_heads, int n_tok, int head_dim, int cache_len, int offset) {
+    if (batch < 0 || n_kv_heads < 0 || n_tok < 0 || x_len < 0 || cache_len < 0)
+        return invalid("negative dimension");
+    if (head_dim != 128) return invalid("only head_dim=128 supported");
+    if (n_tok > x_len) return invalid("n_tok exceeds the token length of x");
+    if (offset < 0 || (long)offset + n_tok > cache_len)
+        return invalid("offset + n_tok exceeds the cache length");
+    if ((long)batch * n_kv_heads > 65535L) return invalid("batch * n_kv_heads exceeds 65535");
+    if ((long)batch * n_kv_heads * n_tok > 0 && (!x || !q || !scale)) return invalid("null pointer");
+    if (!aligned(x, 16) || !aligned(q, 8) || !aligned(scale, 2))
+        return set_error(LLMIK_ERR_ALIGNMENT, "x must be 16-byte aligned, q 8-byte aligned");
+    return LLMIK_OK;
+}
+}  // namespace
+
+LLMIK_API llmik_status llmik_quantize_per_token_int8_into(const void* x, int x_len, void* q_cache,
+                                                          void* scale_cache, int batch,
+                                                          int n_kv_heads, int n_tok, int head_dim,
+                                                          int cache_len, int offset, void* stream) {
+    int st = check_into(x, x_len, q_cache, scale_cache, batch, n_kv_heads, n_tok, head_dim,
+                        cache_len, offset);
+    if (st != LLMIK_OK) return st;
+    return launch_quantize_per_token(x, q_cache, scale_cache, batch * n_kv_heads, n_tok, x_len,
+                                     cache_len, offset, 127, false, as_stream(stream));
+}
+LLMIK_API llmik_status llmik_quantize_v_per_token_int4_into(const void* x, int x_len, void* q_cache,
+                                                            void* scale_cache, int batch,
+                                                            int n_kv_heads, int n_tok, int head_dim,
+                                                            int cache_len, int offset, void* stream) {
+    int st = check_into(x, x_len, q_cache, scale_cache, batch, n_kv_heads, n_tok, head_dim,
+                        cache_len, offset);
+    if (st != LLMIK_OK) return st;
+    return launch_quantize_per_token(x, q_cache, scale_cache, batch * n_kv_heads, n_tok, x_len,
+                                     cache_len, offset, 7, true, as_stream(stream));
+}
+LLMIK_API llmik_status llmik_quantize_k_per_channel_groupwise_int4_into(
+    const void* x, int x_len, void* q_cache, void* scale_cache, int batch, int n_kv_heads,
+    int n_tok, int head_dim, int cache_len, int offset, int group_size, void* stream) {
+    int st = check_into(x, x_len, q_cache, scale_cache, batch, n_kv_heads, n_tok, head_dim,
+                        cache_len, offset);
+    if (st != LLMIK_OK) return st;
+    if (group_size <= 0) return invalid("group_size must be positive");
+    if (offset % group_size != 0) return invalid("offset must be a multiple of group_size");
+    const int cache_groups = (cache_len + group_size - 1) / group_size;
+    return launch_quantize_k_groupwise_int4(x, q_cache, scale_cache, batch * n_kv_heads, n_tok,
+                                            x_len, cache_len, offset, cache_groups, group_size,
+                                            as_stream(stream));
 }
 
 namespace {

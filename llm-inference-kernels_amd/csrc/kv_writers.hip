@@ -8,11 +8,16 @@
 // fast-math (kernels/kv_cache/kv_compress.cu:50-58,128-129,200-201) and are
 // only within +-1 code of the oracle; these kernels divide exactly.
 //
-// Layouts:
-//   x     [rows, 128] fp16 (rows = batch * n_kv_heads * seqlen)
-//   int8  [rows, 128] int8, scale [rows] fp16
-//   int4  [rows, 64] packed (channel 2i -> low nibble of byte i), scale as above
-//   K groupwise int4: scale [batch, n_kv_heads, n_groups, 128] fp16
+// Layouts (one "row" per (batch, kv_head) pair):
+//   x     [rows, src_len, 128] fp16; tokens [0, n_tok) of each row are read
+//   int8  [rows, dst_len, 128] int8, scale [rows, dst_len] fp16
+//   int4  [rows, dst_len, 64] packed (channel 2i -> low nibble of byte i),
+//         scale as above
+//   K groupwise int4: scale [rows, dst_groups, 128] fp16
+// Token t of a row is written to cache position dst_off + t (K groupwise:
+// dst_off is a multiple of group_size and group g goes to scale slot
+// dst_off / group_size + g). The out-of-place ops are the identity map
+// src_len = dst_len = n_tok, dst_off = 0.
 #include "device_common.hpp"
 #include "llmik_internal.hpp"
 
@@ -25,24 +30,42 @@ constexpr int kTokensPerRow = 2;      // per-token writer: tokens per 16-lane ro
 // 8c..8c+7. A workgroup covers 16 * kTokensPerRow consecutive tokens; the
 // row's loads for all its tokens are issued before any is used (token
 // i * 16 + row of the workgroup's block, so each i reads 4 KiB contiguous).
-template <int QMAX, bool PACK4>
+struct TokenMap {
+    uint32_t n_tok;     // tokens per (batch, kv_head) row to quantise
+    uint32_t src_len;   // token stride of x
+    uint32_t dst_len;   // token stride of the destination cache
+    uint32_t dst_off;   // cache position of token 0
+    __device__ __forceinline__ long src(uint32_t flat) const {
+        const uint32_t r = flat / n_tok;
+        return (long)r * src_len + (flat - r * n_tok);
+    }
+    __device__ __forceinline__ long dst(uint32_t flat) const {
+        const uint32_t r = flat / n_tok;
+        return (long)r * dst_len + dst_off + (flat - r * n_tok);
+    }
+};
+
+// MAPPED: tokens go through `map`; otherwise the identity (out-of-place ops,
+// no per-token division).
+template <int QMAX, bool PACK4, bool MAPPED>
 __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, uint16_t* __restrict__ scale,
-    long rows) {
+    long rows, TokenMap map) {
     const long blk = (long)blockIdx.x * (16 * kTokensPerRow);
     const int rr = threadIdx.x >> 4;
     const int c = threadIdx.x & 15;
     u32x4 raw[kTokensPerRow];
 #pragma unroll
     for (int i = 0; i < kTokensPerRow; ++i) {
-        // Rows past the end still take part in the DPP reduction (on a
-        // clamped, in-bounds row) but store nothing.
-        const long row = min(blk + 16 * i + rr, rows - 1);
-        raw[i] = stream16(x + row * 128 + 8 * c);
+        // Tokens past the end still take part in the DPP reduction (on a
+        // clamped, in-bounds token) but store nothing.
+        const long flat = min(blk + 16 * i + rr, rows - 1);
+        const long src = MAPPED ? map.src((uint32_t)flat) : flat;
+        raw[i] = stream16(x + src * 128 + 8 * c);
     }
 #pragma unroll
     for (int i = 0; i < kTokensPerRow; ++i) {
-        const long row = blk + 16 * i + rr;
+        const long flat = blk + 16 * i + rr;
         float xf[8];
         f16x8_to_f32(raw[i], xf);
         float amax = 0.0f;
@@ -59,7 +82,8 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
             v = fminf(fmaxf(v, -(float)QMAX), (float)QMAX);
             code[e] = (int)v;
         }
-        if (row < rows) {
+        if (flat < rows) {
+            const long row = MAPPED ? map.dst((uint32_t)flat) : flat;
             if constexpr (PACK4) {
                 uint32_t w = 0;
 #pragma unroll
@@ -86,14 +110,17 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
 template <int TPR>
 __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, uint16_t* __restrict__ scale,
-    int seqlen, int group_size, int n_groups) {
+    int group_size, TokenMap map, int dst_groups) {
+    const int seqlen = (int)map.n_tok;
     const int g = blockIdx.x;
     const long bh = blockIdx.y;   // batch * n_kv_heads + kv_head
     const int row = threadIdx.x >> 4;
     const int c = threadIdx.x & 15;
     const int t_start = g * group_size;
     const int t_end = min(t_start + group_size, seqlen);
-    const long base = bh * seqlen;
+    const long base = bh * map.src_len;                     // x row of token 0
+    const long qbase = bh * map.dst_len + map.dst_off;      // cache row of token 0
+    const long sslot = bh * dst_groups + map.dst_off / group_size + g;
 
     u32x4 raw[TPR];
 #pragma unroll
@@ -123,7 +150,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
         for (int r = 0; r < 16; ++r) m = fmaxf(m, s_max[r][threadIdx.x]);
         const float sc = fmaxf(m / 7.0f, 1.0e-8f);
         s_scale[threadIdx.x] = sc;
-        scale[(bh * n_groups + g) * 128 + threadIdx.x] = f2h_bits(sc);
+        scale[sslot * 128 + threadIdx.x] = f2h_bits(sc);
     }
     __syncthreads();
 
@@ -146,7 +173,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
             w |= (uint32_t)((int)v & 0xF) << (4 * e);
         }
         if (t < t_end)
-            __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(q + (base + t) * 64 + 4 * c));
+            __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(q + (qbase + t) * 64 + 4 * c));
     }
 }
 
@@ -154,14 +181,17 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
 // codes); the second pass re-reads it from the caches.
 __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_large_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, uint16_t* __restrict__ scale,
-    int seqlen, int group_size, int n_groups) {
+    int group_size, TokenMap map, int dst_groups) {
+    const int seqlen = (int)map.n_tok;
     const int g = blockIdx.x;
     const long bh = blockIdx.y;
     const int row = threadIdx.x >> 4;
     const int c = threadIdx.x & 15;
     const int t_start = g * group_size;
     const int t_end = min(t_start + group_size, seqlen);
-    const long base = bh * seqlen;
+    const long base = bh * map.src_len;                     // x row of token 0
+    const long qbase = bh * map.dst_len + map.dst_off;      // cache row of token 0
+    const long sslot = bh * dst_groups + map.dst_off / group_size + g;
 
     float amax[8];
 #pragma unroll
@@ -184,7 +214,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_larg
         for (int r = 0; r < 16; ++r) m = fmaxf(m, s_max[r][threadIdx.x]);
         const float sc = fmaxf(m / 7.0f, 1.0e-8f);
         s_scale[threadIdx.x] = sc;
-        scale[(bh * n_groups + g) * 128 + threadIdx.x] = f2h_bits(sc);
+        scale[sslot * 128 + threadIdx.x] = f2h_bits(sc);
     }
     __syncthreads();
 
@@ -204,52 +234,57 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_larg
             v = fminf(fmaxf(v, -7.0f), 7.0f);
             w |= (uint32_t)((int)v & 0xF) << (4 * e);
         }
-        *reinterpret_cast<uint32_t*>(q + (base + t) * 64 + 4 * c) = w;
+        *reinterpret_cast<uint32_t*>(q + (qbase + t) * 64 + 4 * c) = w;
     }
 }
 
-int launch_quantize_per_token(const void* x, void* q, void* scale, long rows, int qmax,
-                              bool pack4, hipStream_t stream) {
-    if (rows == 0) return LLMIK_OK;
+int launch_quantize_per_token(const void* x, void* q, void* scale, int rows, int n_tok,
+                              int src_len, int dst_len, int dst_off, int qmax, bool pack4,
+                              hipStream_t stream) {
+    const long total = (long)rows * n_tok;
+    if (total == 0) return LLMIK_OK;
+    if (total > 0x7FFFFFFFL) return set_error(LLMIK_ERR_UNSUPPORTED, "too many tokens");
     const long rows_per_wg = 16 * kTokensPerRow;
-    const long grid = (rows + rows_per_wg - 1) / rows_per_wg;
-    if (grid > 0x7FFFFFFFL) return set_error(LLMIK_ERR_UNSUPPORTED, "too many token rows");
+    const long grid = (total + rows_per_wg - 1) / rows_per_wg;
+    const TokenMap map{(uint32_t)n_tok, (uint32_t)src_len, (uint32_t)dst_len, (uint32_t)dst_off};
     auto xp = static_cast<const uint16_t*>(x);
     auto qp = static_cast<int8_t*>(q);
     auto sp = static_cast<uint16_t*>(scale);
+    const bool mapped = !(src_len == n_tok && dst_len == n_tok && dst_off == 0);
+    const dim3 g((unsigned)grid), b(kWriterThreads);
     if (qmax == 127 && !pack4) {
-        hipLaunchKernelGGL((quantize_per_token_kernel<127, false>), dim3((unsigned)grid),
-                           dim3(kWriterThreads), 0, stream, xp, qp, sp, rows);
+        if (mapped) hipLaunchKernelGGL((quantize_per_token_kernel<127, false, true>), g, b, 0, stream, xp, qp, sp, total, map);
+        else hipLaunchKernelGGL((quantize_per_token_kernel<127, false, false>), g, b, 0, stream, xp, qp, sp, total, map);
     } else if (qmax == 7 && pack4) {
-        hipLaunchKernelGGL((quantize_per_token_kernel<7, true>), dim3((unsigned)grid),
-                           dim3(kWriterThreads), 0, stream, xp, qp, sp, rows);
+        if (mapped) hipLaunchKernelGGL((quantize_per_token_kernel<7, true, true>), g, b, 0, stream, xp, qp, sp, total, map);
+        else hipLaunchKernelGGL((quantize_per_token_kernel<7, true, false>), g, b, 0, stream, xp, qp, sp, total, map);
     } else {
         return set_error(LLMIK_ERR_UNSUPPORTED, "unsupported per-token quantiser variant");
     }
     return check_launch();
 }
 
-int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int batch,
-                                     int n_kv_heads, int seqlen, int group_size,
-                                     hipStream_t stream) {
-    if (seqlen == 0 || batch == 0 || n_kv_heads == 0) return LLMIK_OK;
-    const int n_groups = (seqlen + group_size - 1) / group_size;
-    const long bh = (long)batch * n_kv_heads;
-    if (bh > 65535L) return set_error(LLMIK_ERR_UNSUPPORTED, "batch * n_kv_heads exceeds 65535");
-    const dim3 grid(n_groups, (unsigned)bh), blk(kWriterThreads);
+int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int rows, int n_tok,
+                                     int src_len, int dst_len, int dst_off, int dst_groups,
+                                     int group_size, hipStream_t stream) {
+    if (n_tok == 0 || rows == 0) return LLMIK_OK;
+    if (rows > 65535) return set_error(LLMIK_ERR_UNSUPPORTED, "batch * n_kv_heads exceeds 65535");
+    const int n_groups = (n_tok + group_size - 1) / group_size;
+    const dim3 grid(n_groups, (unsigned)rows), blk(kWriterThreads);
+    const TokenMap map{(uint32_t)n_tok, (uint32_t)src_len, (uint32_t)dst_len, (uint32_t)dst_off};
     auto xp = static_cast<const uint16_t*>(x);
     auto qp = static_cast<int8_t*>(q);
     auto sp = static_cast<uint16_t*>(scale);
     if (group_size <= 16)
-        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<1>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<1>, grid, blk, 0, stream, xp, qp, sp, group_size, map, dst_groups);
     else if (group_size <= 32)
-        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<2>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<2>, grid, blk, 0, stream, xp, qp, sp, group_size, map, dst_groups);
     else if (group_size <= 64)
-        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<4>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<4>, grid, blk, 0, stream, xp, qp, sp, group_size, map, dst_groups);
     else if (group_size <= 128)
-        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<8>, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<8>, grid, blk, 0, stream, xp, qp, sp, group_size, map, dst_groups);
     else
-        hipLaunchKernelGGL(quantize_k_groupwise_int4_large_kernel, grid, blk, 0, stream, xp, qp, sp, seqlen, group_size, n_groups);
+        hipLaunchKernelGGL(quantize_k_groupwise_int4_large_kernel, grid, blk, 0, stream, xp, qp, sp, group_size, map, dst_groups);
     return check_launch();
 }
 

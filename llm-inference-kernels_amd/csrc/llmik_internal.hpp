@@ -59,11 +59,16 @@ int launch_attention_i8(const AttnLaunch& a, hipStream_t stream);
 int launch_attention_i4(const AttnLaunch& a, hipStream_t stream);
 
 // ---- KV writers ------------------------------------------------------------
-int launch_quantize_per_token(const void* x, void* q, void* scale, long rows, int qmax,
-                              bool pack4, hipStream_t stream);
-int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int batch,
-                                     int n_kv_heads, int seqlen, int group_size,
-                                     hipStream_t stream);
+// rows = batch * n_kv_heads; tokens [0, n_tok) of each row of x (token
+// stride src_len) go to cache positions dst_off + t (token stride dst_len).
+int launch_quantize_per_token(const void* x, void* q, void* scale, int rows, int n_tok,
+                              int src_len, int dst_len, int dst_off, int qmax, bool pack4,
+                              hipStream_t stream);
+// As above for K per channel, group-wise; dst_off % group_size == 0 and the
+// scale cache holds dst_groups groups per row.
+int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int rows, int n_tok,
+                                     int src_len, int dst_len, int dst_off, int dst_groups,
+                                     int group_size, hipStream_t stream);
 
 // ---- W4A16 -----------------------------------------------------------------
 struct GemmPlan {

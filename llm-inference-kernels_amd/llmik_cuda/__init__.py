@@ -14,7 +14,11 @@ the reference):
   * `seqlen=-1` on decode_attention_int8 / decode_attention_int4: live
     length inside a preallocated cache, as decode_attention already has;
   * `w4a16_gemm_f32out`: the same GEMM with an fp32 output, used to gate
-    the kernel against an fp32-accumulated oracle without fp16 rounding.
+    the kernel against an fp32-accumulated oracle without fp16 rounding;
+  * `quantize_per_token_into`, `quantize_v_per_token_int4_into`,
+    `quantize_k_per_channel_groupwise_int4_into`: the writers quantising
+    into a preallocated cache at a token offset (no torch.cat), used by the
+    cat-free caches in `llmik_cuda.kv_cache`.
 """
 from __future__ import annotations
 
@@ -28,7 +32,8 @@ __all__ = [
     "decode_attention", "decode_attention_v3", "quantize_per_token", "decode_attention_int8",
     "quantize_k_per_channel_groupwise_int4", "quantize_v_per_token_int4",
     "decode_attention_int4", "w4a16_gemm", "w4a16_dequantize", "rmsnorm", "silu_mul", "rope",
-    "w4a16_gemm_f32out", "LIB_PATH",
+    "w4a16_gemm_f32out", "quantize_per_token_into", "quantize_v_per_token_int4_into",
+    "quantize_k_per_channel_groupwise_int4_into", "LIB_PATH",
 ]
 
 
@@ -262,6 +267,101 @@ def quantize_v_per_token_int4(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tens
         check(lib.llmik_quantize_v_per_token_int4(_ptr(x), _ptr(q), _ptr(scale), batch,
                                                   n_kv_heads, seqlen, head_dim, _stream(x)))
     return q, scale
+
+
+# ------------------------------------------------------- in-place KV writers
+
+def _token_rows(x: torch.Tensor) -> int:
+    """Token stride of x's (batch, kv_head) rows, in tokens. x is either
+    contiguous or a token slice x = buf[:, :, a:b] of a contiguous 4-D
+    buffer: within a row the tokens are contiguous, rows are equally spaced."""
+    batch, n_kv_heads, n_tok, head_dim = x.shape
+    _require(x.stride(3) == 1 and (n_tok <= 1 or x.stride(2) == head_dim),
+             "x must be contiguous within each (batch, kv_head) row")
+    if n_kv_heads > 1:
+        row = x.stride(1)
+        _require(batch <= 1 or x.stride(0) == n_kv_heads * row,
+                 "x rows must be equally spaced (a token slice of a contiguous buffer)")
+    elif batch > 1:
+        row = x.stride(0)
+    else:
+        row = n_tok * head_dim
+    _require(row % head_dim == 0 and row >= n_tok * head_dim,
+             "x rows must be equally spaced (a token slice of a contiguous buffer)")
+    return row // head_dim
+
+
+def _check_into(x: torch.Tensor, q_cache: torch.Tensor, scale_cache: torch.Tensor, offset: int,
+                packed: bool) -> Tuple[int, int, int, int, int, int]:
+    _require(_is_device(x) and _is_device(q_cache) and _is_device(scale_cache),
+             "all inputs must be CUDA tensors")
+    _require(x.dtype == torch.float16, "x must be fp16")
+    _require(q_cache.dtype == torch.int8 and scale_cache.dtype == torch.float16,
+             "q_cache must be int8 and scale_cache fp16")
+    _require(x.dim() == 4 and q_cache.dim() == 4,
+             "x must be [batch, n_kv_heads, n, head_dim] and q_cache 4-D")
+    batch, n_kv_heads, n_tok, head_dim = x.shape
+    _require(head_dim == 128, "only head_dim=128 supported")
+    _require(q_cache.is_contiguous() and scale_cache.is_contiguous(),
+             "q_cache and scale_cache must be contiguous")
+    cache_len = q_cache.size(2)
+    width = head_dim // 2 if packed else head_dim
+    _require(q_cache.size(0) == batch and q_cache.size(1) == n_kv_heads
+             and q_cache.size(3) == width, "q_cache must be [batch, n_kv_heads, cache_len, %d]" % width)
+    _require(0 <= offset and offset + n_tok <= cache_len, "offset + n exceeds the cache length")
+    x_len = _token_rows(x)
+    return batch, n_kv_heads, n_tok, head_dim, cache_len, x_len
+
+
+def quantize_per_token_into(x: torch.Tensor, q_cache: torch.Tensor, scale_cache: torch.Tensor,
+                            offset: int) -> None:
+    """INT8 per-token quantisation of x [batch, n_kv_heads, n, 128] into
+    q_cache [batch, n_kv_heads, cache_len, 128] / scale_cache [batch,
+    n_kv_heads, cache_len] at positions offset..offset+n-1, in place. The
+    codes and scales equal quantize_per_token(x)'s bit for bit."""
+    batch, n_kv_heads, n_tok, head_dim, cache_len, x_len = _check_into(
+        x, q_cache, scale_cache, int(offset), packed=False)
+    _require(tuple(scale_cache.shape) == (batch, n_kv_heads, cache_len),
+             "scale_cache must be [batch, n_kv_heads, cache_len]")
+    with torch.cuda.device(x.device):
+        check(lib.llmik_quantize_per_token_int8_into(
+            _ptr(x), x_len, _ptr(q_cache), _ptr(scale_cache), batch, n_kv_heads, n_tok, head_dim,
+            cache_len, int(offset), _stream(x)))
+
+
+def quantize_v_per_token_int4_into(x: torch.Tensor, q_cache: torch.Tensor,
+                                   scale_cache: torch.Tensor, offset: int) -> None:
+    """KIVI V (INT4 per token, packed) into a preallocated cache at
+    positions offset..offset+n-1; bit-equal to quantize_v_per_token_int4(x)."""
+    batch, n_kv_heads, n_tok, head_dim, cache_len, x_len = _check_into(
+        x, q_cache, scale_cache, int(offset), packed=True)
+    _require(tuple(scale_cache.shape) == (batch, n_kv_heads, cache_len),
+             "scale_cache must be [batch, n_kv_heads, cache_len]")
+    with torch.cuda.device(x.device):
+        check(lib.llmik_quantize_v_per_token_int4_into(
+            _ptr(x), x_len, _ptr(q_cache), _ptr(scale_cache), batch, n_kv_heads, n_tok, head_dim,
+            cache_len, int(offset), _stream(x)))
+
+
+def quantize_k_per_channel_groupwise_int4_into(x: torch.Tensor, q_cache: torch.Tensor,
+                                               scale_cache: torch.Tensor, offset: int,
+                                               group_size: int) -> None:
+    """KIVI K (INT4 per channel, grouped along the sequence) into a
+    preallocated cache. offset is a multiple of group_size; x's n tokens form
+    ceil(n / group_size) groups written to scale slots offset/group_size...,
+    the last one possibly partial. Bit-equal to
+    quantize_k_per_channel_groupwise_int4(x, group_size)."""
+    _require(group_size > 0, "group_size must be positive")
+    _require(int(offset) % group_size == 0, "offset must be a multiple of group_size")
+    batch, n_kv_heads, n_tok, head_dim, cache_len, x_len = _check_into(
+        x, q_cache, scale_cache, int(offset), packed=True)
+    n_groups = (cache_len + group_size - 1) // group_size
+    _require(tuple(scale_cache.shape) == (batch, n_kv_heads, n_groups, head_dim),
+             "scale_cache must be [batch, n_kv_heads, ceil(cache_len/group_size), head_dim]")
+    with torch.cuda.device(x.device):
+        check(lib.llmik_quantize_k_per_channel_groupwise_int4_into(
+            _ptr(x), x_len, _ptr(q_cache), _ptr(scale_cache), batch, n_kv_heads, n_tok, head_dim,
+            cache_len, int(offset), int(group_size), _stream(x)))
 
 
 # -------------------------------------------------------------------- W4A16

@@ -213,3 +213,61 @@ def test_python_validation_messages(as_device, case):
     _, call, msg = case
     with pytest.raises(RuntimeError, match=msg):
         call(as_device)
+
+
+# ------------------------------------------------------- in-place KV writers
+
+def test_c_layer_in_place_writer_errors(lib):
+    S = None
+    # x_len 4 < n_tok 5
+    st = lib.llmik_quantize_per_token_int8_into(16, 4, 16, 16, 1, 8, 5, 128, 64, 0, S)
+    assert st == -1 and "n_tok exceeds" in _err(lib)
+    # offset 60 + 5 > cache_len 64
+    st = lib.llmik_quantize_v_per_token_int4_into(16, 8, 16, 16, 1, 8, 5, 128, 64, 60, S)
+    assert st == -1 and "exceeds the cache length" in _err(lib)
+    st = lib.llmik_quantize_per_token_int8_into(16, 8, 16, 16, 1, 8, 5, 64, 64, 0, S)
+    assert st == -1 and "head_dim=128" in _err(lib)
+    # K groupwise: offset not on a group boundary
+    st = lib.llmik_quantize_k_per_channel_groupwise_int4_into(16, 8, 16, 16, 1, 8, 5, 128, 64, 16,
+                                                              32, S)
+    assert st == -1 and "multiple of group_size" in _err(lib)
+    st = lib.llmik_quantize_k_per_channel_groupwise_int4_into(16, 8, 16, 16, 1, 8, 5, 128, 64, 0,
+                                                              0, S)
+    assert st == -1 and "group_size must be positive" in _err(lib)
+    st = lib.llmik_quantize_per_token_int8_into(16, 8, 20, 16, 1, 8, 5, 128, 64, 0, S)
+    assert st == -4   # q not 8-byte aligned
+
+
+@pytest.mark.parametrize("case", [
+    (lambda m: m.quantize_per_token_into(_t(1, 8, 4, 128), _t(1, 8, 16, 128), _t(1, 8, 16), 0),
+     "q_cache must be int8 and scale_cache fp16"),
+    (lambda m: m.quantize_per_token_into(_t(1, 8, 4, 128), _t(1, 8, 16, 128, dtype=torch.int8),
+                                         _t(1, 8, 16), 13), "offset \\+ n exceeds the cache length"),
+    (lambda m: m.quantize_per_token_into(_t(1, 8, 4, 128), _t(1, 8, 16, 64, dtype=torch.int8),
+                                         _t(1, 8, 16), 0), r"q_cache must be \[batch"),
+    (lambda m: m.quantize_per_token_into(_t(1, 8, 4, 128), _t(1, 8, 16, 128, dtype=torch.int8),
+                                         _t(1, 8, 15), 0), "scale_cache must be"),
+    (lambda m: m.quantize_v_per_token_int4_into(_t(1, 8, 8, 128)[:, :, ::2],
+                                                _t(1, 8, 16, 64, dtype=torch.int8), _t(1, 8, 16), 0),
+     "contiguous within each"),
+    (lambda m: m.quantize_k_per_channel_groupwise_int4_into(
+        _t(1, 8, 4, 128), _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 2, 128), 16, 32),
+     "offset must be a multiple of group_size"),
+    (lambda m: m.quantize_k_per_channel_groupwise_int4_into(
+        _t(1, 8, 4, 128), _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 3, 128), 0, 32),
+     r"scale_cache must be \[batch, n_kv_heads, ceil"),
+])
+def test_python_in_place_writer_validation(as_device, case):
+    call, msg = case
+    with pytest.raises(RuntimeError, match=msg):
+        call(as_device)
+
+
+def test_token_row_stride_of_slices(mod):
+    buf = torch.zeros(2, 3, 40, 128, dtype=torch.float16)
+    assert mod._token_rows(buf) == 40
+    assert mod._token_rows(buf[:, :, 5:17]) == 40
+    assert mod._token_rows(buf[:1, :1, :7]) == 7
+    assert mod._token_rows(buf[:, :1, 3:9]) == 120   # rows of one head: batch stride
+    with pytest.raises(RuntimeError):
+        mod._token_rows(buf[:, ::2])   # unequally spaced rows (3 heads, stride 2)
