@@ -261,6 +261,54 @@ def bench_writers(llmik, B: int, S: int, steps: int, warmup: int, seed: int = 0)
     return out
 
 
+def bench_append(llmik, B: int, S: int, steps: int, warmup: int, seed: int = 0):
+    """One decode step's KV append at cache length S (B batches, 8 kv heads,
+    one new token): the cat-free caches (in-place writers) next to the
+    reference cache's decode step (re-quantise the fp16 residual and
+    torch.cat the whole packed cache, integration/kv_int4_cache.py:168-206),
+    run on the GPU with the same kernels."""
+    import torch
+    from llmik_cuda.kv_cache import Int4KIVICache, Int8KVCache
+    dev = torch.device("cuda:0")
+    g = 128
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    Hkv = 8
+    n_new = max(steps, warmup) + 4
+    k_pre = torch.randn((B, Hkv, S, 128), generator=gen, device=dev, dtype=torch.float16)
+    v_pre = torch.randn((B, Hkv, S, 128), generator=gen, device=dev, dtype=torch.float16)
+    toks = [(torch.randn((B, Hkv, 1, 128), generator=gen, device=dev, dtype=torch.float16),
+             torch.randn((B, Hkv, 1, 128), generator=gen, device=dev, dtype=torch.float16))
+            for _ in range(4)]
+    out = []
+    # cat-free INT4 KIVI and INT8: the cache holds S tokens, each step appends one
+    for name, cache in (("kivi_int4_append_inplace", Int4KIVICache(B, Hkv, S + 2 * n_new + g, g, device=dev)),
+                        ("int8_append_inplace", Int8KVCache(B, Hkv, S + 2 * n_new + g, device=dev))):
+        cache.append(k_pre, v_pre)
+        fns = [lambda c=cache, t=t: c.append(t[0], t[1]) for t in toks]
+        us = time_steps(fns, warmup, steps)
+        out.append({"name": name, "B": B, "S": S, "new_tokens": 1, "us": round(us, 3)})
+        del cache
+    # reference-style KIVI decode step: quantised full groups + an fp16
+    # residual of r tokens, re-quantised and concatenated every step
+    k_full, ks_full = llmik.quantize_k_per_channel_groupwise_int4(k_pre, g)
+    v_full, vs_full = llmik.quantize_v_per_token_int4(v_pre)
+    r = 37
+    k_res = torch.randn((B, Hkv, r, 128), generator=gen, device=dev, dtype=torch.float16)
+    v_res = torch.randn((B, Hkv, r, 128), generator=gen, device=dev, dtype=torch.float16)
+
+    def cat_step():
+        kq, ks = llmik.quantize_k_per_channel_groupwise_int4(k_res, g)
+        vq, vs = llmik.quantize_v_per_token_int4(v_res)
+        return (torch.cat([k_full, kq], dim=2), torch.cat([ks_full, ks], dim=2),
+                torch.cat([v_full, vq], dim=2), torch.cat([vs_full, vs], dim=2))
+    us = time_steps([cat_step], warmup, steps)
+    out.append({"name": "kivi_int4_reference_cat_step", "B": B, "S": S, "residual_tokens": r,
+                "us": round(us, 3)})
+    del k_pre, v_pre, k_full, v_full
+    torch.cuda.empty_cache()
+    return out
+
+
 # -------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(budget_s: float = 15.0):
@@ -293,6 +341,47 @@ def cpu_baseline(budget_s: float = 15.0):
             "sample": f"{len(times)} full calls of oracle/attention.py decode_attention_expanded "
                       f"(eager fp32, repeat_interleave GQA) at B=8 H=32 Hkv=8 D=128 S=4096, "
                       f"median; numpy BLAS threads={threads}"}
+
+
+def cpu_details(budget_s: float = 4.0):
+    """The oracle's writers and W4A16 reference matmul (reference forms:
+    quantisers on x.float(), quantized_matmul_ref with its per-call fp32
+    dequant) on the host, one config each, median of the calls that fit in
+    `budget_s` (at least 2)."""
+    import numpy as np
+    from oracle import kv_quant as okq
+    from oracle import w4a16 as ow
+    rng = np.random.default_rng(0)
+
+    def timed(fn):
+        fn()
+        times, t_end = [], time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter_ns()
+            fn()
+            times.append((time.perf_counter_ns() - t0) / 1e3)
+        times.sort()
+        return round(times[len(times) // 2], 1), len(times)
+
+    out = []
+    x = rng.standard_normal((8, 8, 4096, 128)).astype(np.float16).astype(np.float32)
+    for name, fn in (("quantize_per_token_int8", lambda: okq.quantize_per_token(x, 8)),
+                     ("quantize_k_groupwise_int4_g128",
+                      lambda: okq.quantize_per_channel_groupwise(x, 4, 128)),
+                     ("quantize_v_per_token_int4", lambda: okq.quantize_per_token(x, 4))):
+        us, n = timed(fn)
+        out.append({"name": name, "B": 8, "S": 4096, "cpu_us": us, "calls": n})
+    del x
+    for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
+        W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+        q, s = ow.quantize_weights_int4_groupwise(W, 128)
+        s = s.astype(np.float16)
+        del W
+        act = rng.standard_normal((1, K)).astype(np.float16)
+        us, n = timed(lambda: ow.quantized_matmul_ref(act, q, s, 128))
+        out.append({"name": "w4a16", "M": 1, "K": K, "N": N, "cpu_us": us, "calls": n})
+        del q, s
+    return out
 
 
 # ------------------------------------------------------------- HBM traffic
@@ -348,7 +437,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: attn,int8,int4,w4a16,writers,sweep")
+    ap.add_argument("--only", default="",
+                    help="comma list: int8,int4,w4a16,writers,append,sweep")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the counter-collection program (headline calls + copies) and exit")
     args = ap.parse_args()
@@ -396,12 +486,19 @@ def main() -> None:
         if want("writers"):
             details.extend(bench_writers(llmik, 8, 4096, 50, 5, seed=7))
             log(details[-3:])
+        if want("append"):
+            details.extend(bench_append(llmik, 8, 4096, 50, 5, seed=8))
+            log(details[-3:])
     gpu_wall = time.perf_counter() - t_wall
 
     cpu = None
+    cpu_more = None
     if not args.no_cpu:
         cpu = cpu_baseline()
         log(f"cpu baseline {cpu}")
+        if not args.no_details:
+            cpu_more = cpu_details()
+            log(f"cpu details {cpu_more}")
 
     achieved = head["GBps"]
     line = {
@@ -425,6 +522,7 @@ def main() -> None:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": head["bytes"]},
         "cpu_baseline": cpu,
+        "cpu_details": cpu_more,
         "details": details,
         "gpu_wall_s": round(gpu_wall, 1),
     }
