@@ -31,7 +31,7 @@
 //   p, the INT4 per-channel K scale folds into q per group (q*s split into an
 //   fp16 hi + lo pair so the product keeps fp32 precision).
 // Fallback kernel (decode_attention_valu_kernel): fp32 VALU with 16-lane
-// DPP reductions; used for INT4 group sizes that are not multiples of 16.
+// DPP reductions; used for INT4 group sizes that are not multiples of 32.
 //
 // KV formats (packing is kernels/kv_cache/kv_compress.cuh:25-28 and
 // kernels/common/cuda_utils.cuh:85-119 of the reference):
@@ -262,7 +262,7 @@ struct MfmaTile<KvFormat::F16> {
     u32x4 k[2][4];
     u32x4 v[8];
     __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
-                                         int g, int c) {
+                                         int g, int c, const uint16_t* /*ksrow*/) {
         const uint16_t* kp = static_cast<const uint16_t*>(p.k);
         const uint16_t* vp = static_cast<const uint16_t*>(p.v);
 #pragma unroll
@@ -301,7 +301,7 @@ struct MfmaTile<KvFormat::I8> {
     u32x2 v[8];
     uint16_t ks[2], vs[2];
     __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
-                                         int g, int c) {
+                                         int g, int c, const uint16_t* /*ksrow*/) {
         const int8_t* kp = static_cast<const int8_t*>(p.k);
         const int8_t* vp = static_cast<const int8_t*>(p.v);
 #pragma unroll
@@ -348,10 +348,15 @@ struct MfmaTile<KvFormat::I4> {
     u32x4 k[2];
     uint32_t v[8];
     uint16_t vs[2];
+    u32x4 ksc[4];   // K scales of the tile's group, channels 32g..32g+31 (L2-resident)
+    int grp;        // the tile's scale group (a 32-token tile lies in one group)
     __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
-                                         int g, int c) {
+                                         int g, int c, const uint16_t* ksrow) {
         const int8_t* kp = static_cast<const int8_t*>(p.k);
         const int8_t* vp = static_cast<const int8_t*>(p.v);
+        grp = min(t0, t_last) / p.group_size;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ksc[i] = load16(ksrow + (long)grp * kHeadDim + 8 * i);
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
             const long row = row_base + min(t0 + 16 * blk + c, t_last);
@@ -393,7 +398,8 @@ struct MfmaTile<KvFormat::I4> {
 // contiguous quarter / eighth of the split, so its K-scale group changes
 // only every group_size tokens.
 template <KvFormat F, int HPW, int NW>
-__global__ __launch_bounds__(NW * kWave) void decode_attention_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_attention_mfma_kernel(AttnParams p) {
     const int split = blockIdx.x;
     const int kvh = blockIdx.y / p.n_hchunks;
     const int hchunk = blockIdx.y % p.n_hchunks;
@@ -459,38 +465,35 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_mfma_kernel(AttnP
 
         // ---- scores for the tile's two 16-token blocks ----
         float s[2][4];
+        if constexpr (F == KvFormat::I4) {
+            if (tile.grp != cur_group) {   // wave-uniform; the scales came with the tile
+                cur_group = tile.grp;
+                float sc[32];
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            if constexpr (F == KvFormat::I4) {
-                const int grp = (t0 + 16 * blk) / p.group_size;
-                if (grp != cur_group) {
-                    cur_group = grp;
-                    const uint16_t* ksrow = p.k_scale +
-                        ((long)(b * p.n_kv_heads + kvh) * p.n_groups + grp) * kHeadDim + 32 * g;
-                    float sc[32];
+                for (int i = 0; i < 4; ++i) {
+                    float t[8];
+                    f16x8_to_f32(tile.ksc[i], t);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float t[8];
-                        f16x8_to_f32(load16(ksrow + 8 * i), t);
+                    for (int e = 0; e < 8; ++e) sc[8 * i + e] = t[e];
+                }
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) sc[8 * i + e] = t[e];
+                for (int ks = 0; ks < 4; ++ks) {
+                    f16x8 hi, lo;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int ch = 8 * ks + i4_perm(e);
+                        const float x = qf[ch] * sc[ch];
+                        const f16 xh = (f16)x;
+                        hi[e] = xh;
+                        lo[e] = (f16)(x - (float)xh);
                     }
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) {
-                        f16x8 hi, lo;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const int ch = 8 * ks + i4_perm(e);
-                            const float x = qf[ch] * sc[ch];
-                            const f16 xh = (f16)x;
-                            hi[e] = xh;
-                            lo[e] = (f16)(x - (float)xh);
-                        }
-                        qa[ks] = hi;
-                        qlo[ks] = lo;
-                    }
+                    qa[ks] = hi;
+                    qlo[ks] = lo;
                 }
             }
+        }
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
@@ -550,14 +553,43 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_mfma_kernel(AttnP
         for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(j), o[j]);
     };
 
-    for (int t0 = w0; t0 < w1; t0 += kWaveStride) {
-        MfmaTile<F> tile;
-        tile.load(p, row_base, t0, w1 - 1, g, c);
-        // Keep the V loads next to the K loads: the scheduler would otherwise
-        // sink them below the QK products, which costs a second memory round
-        // trip per tile.
-        __builtin_amdgcn_sched_barrier(0);
-        step(tile, t0);
+    // K-scale row of this (batch, kv head) for lane group g (INT4 only).
+    const uint16_t* ksrow = (F == KvFormat::I4)
+        ? p.k_scale + (long)(b * p.n_kv_heads + kvh) * p.n_groups * kHeadDim + 32 * g : nullptr;
+    // The scheduling barriers keep each tile's V loads next to its K loads
+    // (the scheduler would otherwise sink them below the QK products, which
+    // costs a second memory round trip per tile).
+    if constexpr (F != KvFormat::I4) {
+        // One 16 / 8 KiB fp16 / INT8 tile per wave in flight already keeps
+        // 32 / 16 MiB of loads queued chip-wide; a second one only lengthens
+        // the queue (measured slower for both).
+        for (int t0 = w0; t0 < w1; t0 += kWaveStride) {
+            MfmaTile<F> tile;
+            tile.load(p, row_base, t0, w1 - 1, g, c, ksrow);
+            __builtin_amdgcn_sched_barrier(0);
+            step(tile, t0);
+        }
+    } else if (w0 < w1) {
+        // INT4 tiles are 4 KiB per wave: the next tile's loads are issued
+        // before the current tile's arithmetic. The prefetch is
+        // unconditional (rows past the range clamp to the last row, so it
+        // stays in bounds): a conditional one would make the compiler's wait
+        // count assume it absent and wait for every outstanding load.
+        MfmaTile<F> ta, tb;
+        int t0 = w0;
+        ta.load(p, row_base, t0, w1 - 1, g, c, ksrow);
+        while (true) {
+            tb.load(p, row_base, t0 + kWaveStride, w1 - 1, g, c, ksrow);
+            __builtin_amdgcn_sched_barrier(0);
+            step(ta, t0);
+            t0 += kWaveStride;
+            if (t0 >= w1) break;
+            ta.load(p, row_base, t0 + kWaveStride, w1 - 1, g, c, ksrow);
+            __builtin_amdgcn_sched_barrier(0);
+            step(tb, t0);
+            t0 += kWaveStride;
+            if (t0 >= w1) break;
+        }
     }
 
     // ---- merge the 4 wave states through LDS ----
@@ -867,8 +899,8 @@ static int launch_attention(const AttnLaunch& a, hipStream_t stream) {
     p.gqa = a.n_heads / a.n_kv_heads;
     p.scale_log2 = a.softmax_scale * kLog2e;
 
-    // The MFMA path keeps 16-token blocks inside one INT4 K-scale group.
-    const bool mfma = (F != KvFormat::I4) || (p.group_size % 16 == 0);
+    // The MFMA path keeps each 32-token tile inside one INT4 K-scale group.
+    const bool mfma = (F != KvFormat::I4) || (p.group_size % kTile == 0);
     dim3 grid(pl.n_splits, a.n_kv_heads * pl.n_hchunks, a.batch);
     switch (pl.hpw) {
         case 4: launch_kernel<F, 4>(p, grid, mfma, pl.waves, stream); break;

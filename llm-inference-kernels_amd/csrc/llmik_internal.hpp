@@ -76,14 +76,15 @@ struct GemmPlan {
                        // 2: single-row MFMA GEMV, 3: multi-row MFMA GEMM,
                        // 4: MFMA GEMV over up to 16 rows,
                        // 5: streaming MFMA GEMV, 1 <= M <= 16, N % 64 == 0
+                       // 6: 32x32x16 MFMA GEMM, M > 16, N % 64 == 0
     int cols_per_lane; // 4 (16-byte weight loads) or 1
     int tile_n;        // output columns per workgroup
     int tile_m;        // output rows per workgroup
     int n_tiles, m_tiles;
     int splits;        // K splits
     int kp_per_split;  // packed K rows (8 K each) per split
-    int waves;         // kind 5: waves per workgroup
-    int wave_steps;    // kind 5: 32-K steps per wave
+    int waves;         // kinds 5, 6: waves per workgroup
+    int wave_steps;    // kinds 5, 6: 32-K steps per wave
     size_t workspace_bytes;
     size_t off_part;
 };

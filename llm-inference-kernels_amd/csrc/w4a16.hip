@@ -1188,6 +1188,273 @@ __global__ __launch_bounds__(kMmaThreads) void w4a16_gemm_mfma_kernel(GemmParams
 }
 
 // ---------------------------------------------------------------------------
+// M > 16 on 32x32x16 matrix cores (plan kind 6; N % 64 == 0, group size a
+// power of two >= 32, K % 32 == 0).
+//
+// A workgroup of 8 waves computes a tile of TM = 64 * RH rows by 64 columns
+// over one K split. Wave w = kg * RH + rh owns rows 64 rh .. 64 rh + 63 of
+// the tile and the kg-th of the split's KG = 8 / RH contiguous K ranges
+// (whole scale groups); the KG partial tiles are added in LDS at the end, in
+// a fixed tree order. Per 32-K step a wave loads, straight into registers:
+//   * two 8-byte weight words per lane: lane (h = l / 32, c = l % 32) takes
+//     packed rows 4 st + 2 kc + h (kc = 0, 1) of columns n0 + 2c and
+//     n0 + 2c + 1: the B fragments of two MFMAs per 16-K chunk whose 32
+//     columns are n0 + 2c' + j (j = 0, 1);
+//   * four 16-byte activation fragments (rows 32 rb + c, K 16 kc + 8h ..
+//     + 7; rows >= M read zero through the buffer bound). Each activation
+//     element is used by exactly one wave, so nothing is staged in LDS;
+//   * the step's group scales of its two columns (4 bytes).
+// The codes become exact fp16 (i4x8_to_f16_pairs, pair order (i, i + 4));
+// the activation fragment is permuted to the same order. A step is 8
+// v_mfma_f32_32x32x16_f16 (2 row blocks x 2 column sets x 2 chunks) into
+// per-group fp32 accumulators, scaled at the group's end:
+//   acc += scale[g][n] * C_g.
+// Each dequantised word serves 64 rows, which keeps the conversion below
+// the matrix-core time. Two steps of loads are in flight per wave.
+// ---------------------------------------------------------------------------
+constexpr int kG32Waves = 8;
+constexpr int kG32Threads = kG32Waves * kWave;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct G32Step {
+    u32x2 w[2];        // [kc]: words of columns 2c, 2c + 1
+    u32x4 a[2][2];     // [rb][kc]
+    uint32_t s;        // scales of columns 2c, 2c + 1 for the step's group
+};
+
+template <int RH>
+__global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmParams p) {
+    constexpr int KG = kG32Waves / RH;
+    constexpr int TM = 64 * RH;
+    constexpr int kVals = 2 * 2 * 16;                 // accumulator values per lane
+    __shared__ float s_red[KG / 2][RH][kVals][kWave];   // 64 KiB
+    __shared__ uint32_t s_last;
+
+    // (tile, split, m-tile) from an XCD-contiguous order of workgroup ids.
+    int bid = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+    const int tile = bid % p.n_tiles;
+    const int rest = bid / p.n_tiles;
+    const int split = rest % p.splits;
+    const int mtile = rest / p.splits;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rh = wave % RH;
+    const int kg = wave / RH;
+    const int c = lane & 31;
+    const int h = lane >> 5;
+
+    const int steps = p.K / 32;
+    const int sps = p.kp_per_split / 4;
+    const int k0 = split * sps;
+    const int nst = min(sps, steps - k0);
+    const int ws0 = k0 + min(kg * p.wave_steps, nst);
+    const int ws1 = k0 + min((kg + 1) * p.wave_steps, nst);
+    const int n0 = tile * 64;
+    const int mrow0 = mtile * TM + 64 * rh;
+    const int n_grp = p.K / p.group_size;
+    const int spg_mask = (1 << p.gshift) - 1;
+
+    const __amdgpu_buffer_rsrc_t rw = make_buffer_rsrc(p.w, (uint32_t)(p.K / 8) * p.N * 4u);
+    const __amdgpu_buffer_rsrc_t ra = make_buffer_rsrc(p.act, (uint32_t)p.M * p.K * 2u);
+    const __amdgpu_buffer_rsrc_t rs = make_buffer_rsrc(p.scale, (uint32_t)n_grp * p.N * 2u);
+    const uint32_t w_off = ((uint32_t)h * p.N + n0 + 2 * c) * 4u;
+    const uint32_t w_kc = (uint32_t)p.N * 8u;    // bytes between the packed rows of two chunks
+    const uint32_t w_step = (uint32_t)p.N * 16u;
+    uint32_t a_off[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int row = mrow0 + 32 * rb + c;
+        // Rows past M point beyond the buffer bound and load zeros.
+        a_off[rb] = (row < p.M) ? ((uint32_t)row * p.K + 8u * h) * 2u : 0x80000000u;
+    }
+    const uint32_t s_off = (uint32_t)(n0 + 2 * c) * 2u;
+    const uint32_t grp_bytes = (uint32_t)p.N * 2u;
+
+    auto load_step = [&](G32Step& t, int st_req) {
+        const uint32_t st = (uint32_t)min(st_req, ws1 - 1);   // in bounds, re-read past the end
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            t.w[kc] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                rw, (int)(w_off + kc * w_kc), (int)(st * w_step), 2));
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+                t.a[rb][kc] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_off[rb] + 32u * kc),
+                                                                    (int)(st * 64u), 0);
+        }
+        t.s = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)s_off, (int)((st >> p.gshift) * grp_bytes), 0);
+    };
+
+    f32x16 acc[2][2], cg[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[rb][j][r] = 0.0f;
+                cg[rb][j][r] = 0.0f;
+            }
+
+    auto consume = [&](const G32Step& t, int st) {
+        if (st >= ws1) return;   // wave-uniform: a prefetched step past the range
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            f16x8 bop[2], aop[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                f16x2 wp[4];
+                i4x8_to_f16_pairs(t.w[kc][j], wp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bop[j][2 * i] = wp[i][0];
+                    bop[j][2 * i + 1] = wp[i][1];
+                }
+            }
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                const u32x4 a = t.a[rb][kc];
+                aop[rb] = __builtin_bit_cast(f16x8, make_u32x4(
+                    perm_b32(a[2], a[0], 0x05040100u), perm_b32(a[2], a[0], 0x07060302u),
+                    perm_b32(a[3], a[1], 0x05040100u), perm_b32(a[3], a[1], 0x07060302u)));
+            }
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    cg[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], bop[j], cg[rb][j], 0, 0, 0);
+        }
+        if (((st & spg_mask) == spg_mask) || st == ws1 - 1) {   // end of a scale group
+            const float s0 = h2f((uint16_t)t.s);
+            const float s1 = h2f((uint16_t)(t.s >> 16));
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc[rb][0][r] = fmaf(s0, cg[rb][0][r], acc[rb][0][r]);
+                    acc[rb][1][r] = fmaf(s1, cg[rb][1][r], acc[rb][1][r]);
+                    cg[rb][0][r] = 0.0f;
+                    cg[rb][1][r] = 0.0f;
+                }
+        }
+    };
+
+    if (ws0 < ws1) {
+        G32Step t0, t1;
+        load_step(t0, ws0);
+        load_step(t1, ws0 + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        for (int st = ws0; st < ws1; st += 2) {
+            consume(t0, st);
+            load_step(t0, st + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(t1, st + 1);
+            load_step(t1, st + 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Add the KG partial tiles of each row half: waves kg in [half, 2 half)
+    // hand theirs to kg - half, halving until kg == 0 holds the sum.
+#pragma unroll
+    for (int half = KG / 2; half >= 1; half /= 2) {
+        if (kg >= half && kg < 2 * half) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s_red[kg - half][rh][(rb * 2 + j) * 16 + r][lane] = acc[rb][j][r];
+        }
+        __syncthreads();
+        if (kg < half) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[rb][j][r] += s_red[kg][rh][(rb * 2 + j) * 16 + r][lane];
+        }
+        __syncthreads();
+    }
+
+    // C layout of v_mfma_f32_32x32x16: value r of lane l is row
+    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 of the 32 x 32 block.
+    auto out_row = [&](int rb, int r) { return mrow0 + 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3); };
+    if (p.splits == 1) {
+        if (kg == 0) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = out_row(rb, r);
+                    if (m < p.M) {
+                        store_out(p, m, n0 + 2 * c, acc[rb][0][r]);
+                        store_out(p, m, n0 + 2 * c + 1, acc[rb][1][r]);
+                    }
+                }
+        }
+        return;
+    }
+    if (kg == 0) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = out_row(rb, r);
+                if (m < p.M) {
+                    float* dst = &p.part[((long)split * p.M + m) * p.N + n0 + 2 * c];
+                    publish_store(dst, acc[rb][0][r]);
+                    publish_store(dst + 1, acc[rb][1][r]);
+                }
+            }
+    }
+    publish_wait();
+    __syncthreads();
+    const int counter = mtile * p.n_tiles + tile;
+    if (threadIdx.x == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u) return;
+    // Last split of the tile: each thread adds the splits of its kPer
+    // outputs in split order, with the loads of two splits for all of them
+    // issued together (a few memory round trips per tile, not one per output).
+    constexpr int kPer = TM * 64 / kG32Threads;
+    const long mn = (long)p.M * p.N;
+    float tot[kPer];
+    long idx[kPer];
+#pragma unroll
+    for (int o = 0; o < kPer; ++o) {
+        const int e = threadIdx.x + o * kG32Threads;
+        const int m = min(mtile * TM + e / 64, p.M - 1);
+        idx[o] = (long)m * p.N + n0 + e % 64;
+        tot[o] = 0.0f;
+    }
+    for (int s0 = 0; s0 < p.splits; s0 += 2) {
+        float x[2][kPer];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const long base = (long)min(s0 + u, p.splits - 1) * mn;
+#pragma unroll
+            for (int o = 0; o < kPer; ++o) x[u][o] = publish_load(p.part + base + idx[o]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int o = 0; o < kPer; ++o)
+                if (s0 + u < p.splits) tot[o] += x[u][o];
+    }
+#pragma unroll
+    for (int o = 0; o < kPer; ++o) {
+        const int e = threadIdx.x + o * kG32Threads;
+        const int m = mtile * TM + e / 64;
+        if (m < p.M) store_out(p, m, n0 + e % 64, tot[o]);
+    }
+    if (threadIdx.x == 0) p.counters[counter] = 0u;
+}
+
+// ---------------------------------------------------------------------------
 // M > 1: each lane owns COLS columns and MT rows; the weight is dequantised
 // once per packed word into fp32 (code * scale, exact) and reused across the
 // MT rows. Grid z walks the row tiles.
@@ -1466,6 +1733,37 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
             (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
         return pl;
     }
+    if (M > 16 && N % 64 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31) &&
+        (long)M * K * 2 < (1L << 31)) {
+        // 32x32x16 matrix-core GEMM: tiles of 64 * rh rows by 64 columns,
+        // 8 waves = rh row halves x (8 / rh) K ranges of whole scale groups;
+        // K splits until the tiles fill the CUs once (no second round).
+        const int rh = (M > 64) ? 2 : 1;
+        const int kgs = kG32Waves / rh;
+        const int steps = K / 32;
+        const int spg = group_size / 32;
+        pl.kind = 6;
+        pl.cols_per_lane = 2;
+        pl.tile_n = 64;
+        pl.tile_m = 64 * rh;
+        pl.n_tiles = N / 64;
+        pl.m_tiles = (M + pl.tile_m - 1) / pl.tile_m;
+        const long base = (long)pl.n_tiles * pl.m_tiles;
+        long want = device_cu_count() / base;
+        if (base > kMaxCounters) want = 1;
+        if (want < 1) want = 1;
+        int ws = (int)((steps + want * kgs - 1) / (want * kgs));
+        if (ws > spg) ws = (ws + spg - 1) / spg * spg;
+        if (ws < 1) ws = 1;
+        pl.wave_steps = ws;
+        pl.waves = kG32Waves;
+        pl.kp_per_split = 4 * ws * kgs;
+        pl.splits = (steps + ws * kgs - 1) / (ws * kgs);
+        pl.off_part = kCounterBytes;
+        pl.workspace_bytes =
+            (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
+        return pl;
+    }
     if (M >= 2 && N % 64 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31)) {
         // Matrix-core GEMM: tiles of 16 * rt rows by 64 columns.
         int rt = 1;
@@ -1565,6 +1863,10 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
         const int grid = pl.n_tiles * pl.splits;
         if (pl.kp_per_split / 4 / kGemvWaves > kGemvBatch) launch_gemv16_cb<2, true>(p, grid, stream);
         else launch_gemv16_cb<2, false>(p, grid, stream);
+    } else if (pl.kind == 6) {
+        const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kG32Threads);
+        if (pl.tile_m == 128) hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel<2>, grid, blk, 0, stream, p);
+        else hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel<1>, grid, blk, 0, stream, p);
     } else if (pl.kind == 3) {
         const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kMmaThreads);
         switch (pl.tile_m) {
