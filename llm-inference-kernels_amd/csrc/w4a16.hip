@@ -36,7 +36,8 @@ struct GemmParams {
     int f32_out;
     int gshift;          // log2(group_size / 32) on the matrix-core GEMV
     int nw;              // streaming GEMV: waves per workgroup
-    int wave_steps;      // streaming GEMV: 32-K steps per wave
+    int wave_steps;      // streaming GEMV / 32x32 GEMM: 32-K steps per wave
+    int m_tiles_;        // 32x32 GEMM: row tiles
 };
 
 // Eight int4 codes of one word -> four fp16 pairs, exact. Pair j holds the
@@ -1188,61 +1189,64 @@ __global__ __launch_bounds__(kMmaThreads) void w4a16_gemm_mfma_kernel(GemmParams
 }
 
 // ---------------------------------------------------------------------------
-// M > 16 on 32x32x16 matrix cores (plan kind 6; N % 64 == 0, group size a
+// M > 16 on 32x32x16 matrix cores (plan kind 6; N % 128 == 0, group size a
 // power of two >= 32, K % 32 == 0).
 //
-// A workgroup of 8 waves computes a tile of TM = 64 * RH rows by 64 columns
-// over one K split. Wave w = kg * RH + rh owns rows 64 rh .. 64 rh + 63 of
-// the tile and the kg-th of the split's KG = 8 / RH contiguous K ranges
-// (whole scale groups); the KG partial tiles are added in LDS at the end, in
-// a fixed tree order. Per 32-K step a wave loads, straight into registers:
-//   * two 8-byte weight words per lane: lane (h = l / 32, c = l % 32) takes
-//     packed rows 4 st + 2 kc + h (kc = 0, 1) of columns n0 + 2c and
-//     n0 + 2c + 1: the B fragments of two MFMAs per 16-K chunk whose 32
-//     columns are n0 + 2c' + j (j = 0, 1);
-//   * four 16-byte activation fragments (rows 32 rb + c, K 16 kc + 8h ..
-//     + 7; rows >= M read zero through the buffer bound). Each activation
-//     element is used by exactly one wave, so nothing is staged in LDS;
-//   * the step's group scales of its two columns (4 bytes).
-// The codes become exact fp16 (i4x8_to_f16_pairs, pair order (i, i + 4));
-// the activation fragment is permuted to the same order. A step is 8
-// v_mfma_f32_32x32x16_f16 (2 row blocks x 2 column sets x 2 chunks) into
-// per-group fp32 accumulators, scaled at the group's end:
+// A workgroup of 8 waves computes a tile of 64 rows by 128 columns over one
+// K split. Wave w = 2 kg + ch owns columns 64 ch .. 64 ch + 63 of the tile,
+// all 64 rows, and the kg-th of the split's 4 contiguous K ranges (whole
+// scale groups where the split allows); the 4 partial tiles of a column half
+// are added in LDS at the end in a fixed tree order.
+//
+// Activations. The two waves of a K range share its activation rows: per
+// stage of two 32-K steps each loads 32 rows x 128 bytes with full-line
+// 16-byte loads, permutes every 8 values to the pair order of the weight
+// codes (i, i + 4) and writes them to the K range's LDS slot (row stride
+// 144 bytes: the fragment reads of 8 consecutive rows hit distinct banks).
+// A fragment of v_mfma_f32_32x32x16_f16 is then one 16-byte LDS read: lane
+// (h = l / 32, c = l % 32) takes row 32 rb + c, K 16 kc + 8 h of the step.
+// Stage s + 1 is loaded while stage s is computed (double-buffered slots).
+//
+// Weights. Lane (h, c) loads, per step and 16-K chunk kc, the 8-byte pair of
+// words of columns 2c and 2c + 1 (packed row 4 st + 2 kc + h): the B
+// fragments of two MFMAs whose 32 columns are 2c' + j (j = 0, 1). Words are
+// held in a three-stage register ring, two stages ahead of their use. They
+// become exact fp16 codes (i4x8_to_f16_pairs); products accumulate per
+// scale group in fp32 (the group's first chunk starts from zero) and are
+// scaled at the group's end:
 //   acc += scale[g][n] * C_g.
-// Each dequantised word serves 64 rows, which keeps the conversion below
-// the matrix-core time. Two steps of loads are in flight per wave.
+// Each dequantised word serves the 64 rows of the tile.
 // ---------------------------------------------------------------------------
+constexpr int kG32RowHalves = 72;
 constexpr int kG32Waves = 8;
 constexpr int kG32Threads = kG32Waves * kWave;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-struct G32Step {
-    u32x2 w[2];        // [kc]: words of columns 2c, 2c + 1
-    u32x4 a[2][2];     // [rb][kc]
-    uint32_t s;        // scales of columns 2c, 2c + 1 for the step's group
+struct G32W {
+    u32x2 w[2][2];     // [step][kc]: words of columns 2c, 2c + 1
+    uint32_t s[2];     // [step]: scales of columns 2c, 2c + 1
 };
 
-template <int RH>
 __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmParams p) {
-    constexpr int KG = kG32Waves / RH;
-    constexpr int TM = 64 * RH;
-    constexpr int kVals = 2 * 2 * 16;                 // accumulator values per lane
-    __shared__ float s_red[KG / 2][RH][kVals][kWave];   // 64 KiB
+    constexpr int TM = 64;
+    constexpr int KG = 4;
+    __shared__ __attribute__((aligned(16))) uint16_t s_a[KG][2][TM][kG32RowHalves];   // 72 KiB
     __shared__ uint32_t s_last;
 
-    // (tile, split, m-tile) from an XCD-contiguous order of workgroup ids.
+    // (tile, split, m-tile) from an XCD-contiguous order of workgroup ids:
+    // the m-tiles of a column tile are neighbours and share its weights in L2.
     int bid = blockIdx.x;
     const int nwg = gridDim.x;
     if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
-    const int tile = bid % p.n_tiles;
-    const int rest = bid / p.n_tiles;
-    const int split = rest % p.splits;
-    const int mtile = rest / p.splits;
+    const int mtile = bid % p.m_tiles_;
+    const int rest = bid / p.m_tiles_;
+    const int tile = rest % p.n_tiles;
+    const int split = rest / p.n_tiles;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rh = wave % RH;
-    const int kg = wave / RH;
+    const int ch = wave & 1;
+    const int kg = wave >> 1;
     const int c = lane & 31;
     const int h = lane >> 5;
 
@@ -1252,8 +1256,8 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
     const int nst = min(sps, steps - k0);
     const int ws0 = k0 + min(kg * p.wave_steps, nst);
     const int ws1 = k0 + min((kg + 1) * p.wave_steps, nst);
-    const int n0 = tile * 64;
-    const int mrow0 = mtile * TM + 64 * rh;
+    const int n0 = tile * 128 + 64 * ch;
+    const int m0 = mtile * TM;
     const int n_grp = p.K / p.group_size;
     const int spg_mask = (1 << p.gshift) - 1;
 
@@ -1263,101 +1267,155 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
     const uint32_t w_off = ((uint32_t)h * p.N + n0 + 2 * c) * 4u;
     const uint32_t w_kc = (uint32_t)p.N * 8u;    // bytes between the packed rows of two chunks
     const uint32_t w_step = (uint32_t)p.N * 16u;
-    uint32_t a_off[2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        const int row = mrow0 + 32 * rb + c;
-        // Rows past M point beyond the buffer bound and load zeros.
-        a_off[rb] = (row < p.M) ? ((uint32_t)row * p.K + 8u * h) * 2u : 0x80000000u;
-    }
     const uint32_t s_off = (uint32_t)(n0 + 2 * c) * 2u;
     const uint32_t grp_bytes = (uint32_t)p.N * 2u;
+    // Activation staging: this wave loads rows 32 ch + (l >> 3) + 8 i of the
+    // stage, 16-byte column q = l & 7 (rows past M point beyond the buffer
+    // bound and load zeros).
+    const int q = lane & 7;
+    uint32_t a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + 32 * ch + (lane >> 3) + 8 * i;
+        a_off[i] = (row < p.M) ? ((uint32_t)row * p.K + 8u * q) * 2u : 0x80000000u;
+    }
 
-    auto load_step = [&](G32Step& t, int st_req) {
-        const uint32_t st = (uint32_t)min(st_req, ws1 - 1);   // in bounds, re-read past the end
+    // Steps past the wave's range re-read its last step (in bounds) and are
+    // never consumed.
+    auto clamp_step = [&](int st) { return (uint32_t)max(min(st, ws1 - 1), 0); };
+    auto load_w = [&](G32W& t, int st0) {
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            t.w[kc] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                rw, (int)(w_off + kc * w_kc), (int)(st * w_step), 2));
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t st = clamp_step(st0 + j);
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-                t.a[rb][kc] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_off[rb] + 32u * kc),
-                                                                    (int)(st * 64u), 0);
+            for (int kc = 0; kc < 2; ++kc)
+                t.w[j][kc] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                    rw, (int)(w_off + kc * w_kc), (int)(st * w_step), 2));
+            t.s[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)s_off,
+                                                          (int)((st >> p.gshift) * grp_bytes), 0);
         }
-        t.s = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)s_off, (int)((st >> p.gshift) * grp_bytes), 0);
+    };
+    u32x4 areg[4];
+    auto load_a = [&](int st0) {
+        const uint32_t st = clamp_step(st0);   // a stage starts at an even step of the range
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)a_off[i], (int)(st * 64u), 0);
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 a = areg[i];
+            const u32x4 r = make_u32x4(perm_b32(a[2], a[0], 0x05040100u), perm_b32(a[2], a[0], 0x07060302u),
+                                       perm_b32(a[3], a[1], 0x05040100u), perm_b32(a[3], a[1], 0x07060302u));
+            *reinterpret_cast<u32x4*>(&s_a[kg][buf][32 * ch + (lane >> 3) + 8 * i][8 * q]) = r;
+        }
     };
 
     f32x16 acc[2][2], cg[2][2];
+    const f32x16 zero16 = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
+                           0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc[rb][j][r] = 0.0f;
-                cg[rb][j][r] = 0.0f;
-            }
-
-    auto consume = [&](const G32Step& t, int st) {
-        if (st >= ws1) return;   // wave-uniform: a prefetched step past the range
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            f16x8 bop[2], aop[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                f16x2 wp[4];
-                i4x8_to_f16_pairs(t.w[kc][j], wp);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    bop[j][2 * i] = wp[i][0];
-                    bop[j][2 * i + 1] = wp[i][1];
-                }
-            }
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                const u32x4 a = t.a[rb][kc];
-                aop[rb] = __builtin_bit_cast(f16x8, make_u32x4(
-                    perm_b32(a[2], a[0], 0x05040100u), perm_b32(a[2], a[0], 0x07060302u),
-                    perm_b32(a[3], a[1], 0x05040100u), perm_b32(a[3], a[1], 0x07060302u)));
-            }
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    cg[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], bop[j], cg[rb][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) {
+            acc[rb][j] = zero16;
+            cg[rb][j] = zero16;
         }
-        if (((st & spg_mask) == spg_mask) || st == ws1 - 1) {   // end of a scale group
-            const float s0 = h2f((uint16_t)t.s);
-            const float s1 = h2f((uint16_t)(t.s >> 16));
+
+    auto compute = [&](const G32W& t, int buf, int st0) {
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
+        for (int js = 0; js < 2; ++js) {
+            const int st = st0 + js;
+            if (st >= ws1) break;   // wave-uniform
+            // The first chunk of a scale group starts its accumulators from
+            // zero (an inline-zero C operand), so nothing is cleared at the
+            // group's end.
+            const bool first = ((st & spg_mask) == 0) || st == ws0;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    acc[rb][0][r] = fmaf(s0, cg[rb][0][r], acc[rb][0][r]);
-                    acc[rb][1][r] = fmaf(s1, cg[rb][1][r], acc[rb][1][r]);
-                    cg[rb][0][r] = 0.0f;
-                    cg[rb][1][r] = 0.0f;
+            for (int kc = 0; kc < 2; ++kc) {
+                f16x8 bop[2], aop[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    f16x2 wp[4];
+                    i4x8_to_f16_pairs(t.w[js][kc][j], wp);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        bop[j][2 * i] = wp[i][0];
+                        bop[j][2 * i + 1] = wp[i][1];
+                    }
                 }
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+                    aop[rb] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(
+                        &s_a[kg][buf][32 * rb + c][32 * js + 16 * kc + 8 * h]));
+                if (kc == 0 && first) {
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            cg[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], bop[j], zero16, 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            cg[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], bop[j], cg[rb][j], 0, 0, 0);
+                }
+            }
+            if (((st & spg_mask) == spg_mask) || st == ws1 - 1) {   // end of a scale group
+                const float s0 = h2f((uint16_t)t.s[js]);
+                const float s1 = h2f((uint16_t)(t.s[js] >> 16));
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        acc[rb][0][r] = fmaf(s0, cg[rb][0][r], acc[rb][0][r]);
+                        acc[rb][1][r] = fmaf(s1, cg[rb][1][r], acc[rb][1][r]);
+                    }
+            }
         }
     };
 
-    if (ws0 < ws1) {
-        G32Step t0, t1;
-        load_step(t0, ws0);
-        load_step(t1, ws0 + 1);
+    // Stage loop: every wave runs the same number of stages (the longest K
+    // range of the workgroup) so that the barriers match; a wave whose range
+    // is shorter or empty computes nothing in the extra stages.
+    const int n_stages = (p.wave_steps + 1) / 2;
+    {
+        G32W wr[3];
+        load_w(wr[0], ws0);
+        load_w(wr[1], ws0 + 2);
+        load_a(ws0);
         __builtin_amdgcn_sched_barrier(0);
-        for (int st = ws0; st < ws1; st += 2) {
-            consume(t0, st);
-            load_step(t0, st + 2);
+        store_a(0);
+        load_a(ws0 + 2);
+        __syncthreads();
+        // One pass of the unrolled body handles stages s, s + 1, s + 2 with
+        // ring slots 0, 1, 2 and LDS buffers alternating from `buf`.
+        auto stage = [&](G32W& cur, G32W& ahead2, int s, int buf) {
+            load_w(ahead2, ws0 + 2 * (s + 2));
             __builtin_amdgcn_sched_barrier(0);
-            consume(t1, st + 1);
-            load_step(t1, st + 3);
-            __builtin_amdgcn_sched_barrier(0);
+            compute(cur, buf, ws0 + 2 * s);
+            store_a(buf ^ 1);          // stage s + 1, loaded during stage s - 1 / the prologue
+            load_a(ws0 + 2 * (s + 2));
+            __syncthreads();
+        };
+        int s = 0;
+        int buf = 0;
+        while (true) {
+            if (s >= n_stages) break;
+            stage(wr[0], wr[2], s, buf); ++s; buf ^= 1;
+            if (s >= n_stages) break;
+            stage(wr[1], wr[0], s, buf); ++s; buf ^= 1;
+            if (s >= n_stages) break;
+            stage(wr[2], wr[1], s, buf); ++s; buf ^= 1;
         }
     }
 
-    // Add the KG partial tiles of each row half: waves kg in [half, 2 half)
-    // hand theirs to kg - half, halving until kg == 0 holds the sum.
+    // Add the 4 K-range tiles of each column half (waves kg in [half, 2 half)
+    // hand theirs to kg - half) through LDS, reusing the activation slots.
+    float* s_red = reinterpret_cast<float*>(&s_a[0][0][0][0]);   // [2][2][64 values][64 lanes]
+    constexpr int kVals = 2 * 2 * 16;
 #pragma unroll
     for (int half = KG / 2; half >= 1; half /= 2) {
         if (kg >= half && kg < 2 * half) {
@@ -1366,7 +1424,9 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) s_red[kg - half][rh][(rb * 2 + j) * 16 + r][lane] = acc[rb][j][r];
+                    for (int r = 0; r < 16; ++r)
+                        s_red[(((kg - half) * 2 + ch) * kVals + (rb * 2 + j) * 16 + r) * kWave + lane] =
+                            acc[rb][j][r];
         }
         __syncthreads();
         if (kg < half) {
@@ -1375,14 +1435,15 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[rb][j][r] += s_red[kg][rh][(rb * 2 + j) * 16 + r][lane];
+                    for (int r = 0; r < 16; ++r)
+                        acc[rb][j][r] += s_red[((kg * 2 + ch) * kVals + (rb * 2 + j) * 16 + r) * kWave + lane];
         }
         __syncthreads();
     }
 
     // C layout of v_mfma_f32_32x32x16: value r of lane l is row
     // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 of the 32 x 32 block.
-    auto out_row = [&](int rb, int r) { return mrow0 + 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3); };
+    auto out_row = [&](int rb, int r) { return m0 + 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3); };
     if (p.splits == 1) {
         if (kg == 0) {
 #pragma unroll
@@ -1413,22 +1474,23 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
     }
     publish_wait();
     __syncthreads();
-    const int counter = mtile * p.n_tiles + tile;
+    const int counter = tile * p.m_tiles_ + mtile;
     if (threadIdx.x == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
     // Last split of the tile: each thread adds the splits of its kPer
     // outputs in split order, with the loads of two splits for all of them
     // issued together (a few memory round trips per tile, not one per output).
-    constexpr int kPer = TM * 64 / kG32Threads;
+    constexpr int kPer = TM * 128 / kG32Threads;
     const long mn = (long)p.M * p.N;
+    const int nt0 = tile * 128;
     float tot[kPer];
     long idx[kPer];
 #pragma unroll
     for (int o = 0; o < kPer; ++o) {
         const int e = threadIdx.x + o * kG32Threads;
-        const int m = min(mtile * TM + e / 64, p.M - 1);
-        idx[o] = (long)m * p.N + n0 + e % 64;
+        const int m = min(m0 + e / 128, p.M - 1);
+        idx[o] = (long)m * p.N + nt0 + e % 128;
         tot[o] = 0.0f;
     }
     for (int s0 = 0; s0 < p.splits; s0 += 2) {
@@ -1448,8 +1510,8 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
 #pragma unroll
     for (int o = 0; o < kPer; ++o) {
         const int e = threadIdx.x + o * kG32Threads;
-        const int m = mtile * TM + e / 64;
-        if (m < p.M) store_out(p, m, n0 + e % 64, tot[o]);
+        const int m = m0 + e / 128;
+        if (m < p.M) store_out(p, m, nt0 + e % 128, tot[o]);
     }
     if (threadIdx.x == 0) p.counters[counter] = 0u;
 }
@@ -1733,28 +1795,27 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
             (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
         return pl;
     }
-    if (M > 16 && N % 64 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31) &&
+    if (M > 16 && N % 128 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31) &&
         (long)M * K * 2 < (1L << 31)) {
-        // 32x32x16 matrix-core GEMM: tiles of 64 * rh rows by 64 columns,
-        // 8 waves = rh row halves x (8 / rh) K ranges of whole scale groups;
-        // K splits until the tiles fill the CUs once (no second round).
-        const int rh = (M > 64) ? 2 : 1;
-        const int kgs = kG32Waves / rh;
+        // 32x32x16 matrix-core GEMM: tiles of 64 rows by 128 columns, 8 waves
+        // = 2 column halves x 4 K ranges of whole scale groups; K splits
+        // until the tiles fill the CUs once (no second round).
+        constexpr int kgs = 4;
         const int steps = K / 32;
         const int spg = group_size / 32;
         pl.kind = 6;
         pl.cols_per_lane = 2;
-        pl.tile_n = 64;
-        pl.tile_m = 64 * rh;
-        pl.n_tiles = N / 64;
-        pl.m_tiles = (M + pl.tile_m - 1) / pl.tile_m;
+        pl.tile_n = 128;
+        pl.tile_m = 64;
+        pl.n_tiles = N / 128;
+        pl.m_tiles = (M + 63) / 64;
         const long base = (long)pl.n_tiles * pl.m_tiles;
         long want = device_cu_count() / base;
         if (base > kMaxCounters) want = 1;
         if (want < 1) want = 1;
         int ws = (int)((steps + want * kgs - 1) / (want * kgs));
         if (ws > spg) ws = (ws + spg - 1) / spg * spg;
-        if (ws < 1) ws = 1;
+        ws = (ws + 1) / 2 * 2;   // whole two-step stages
         pl.wave_steps = ws;
         pl.waves = kG32Waves;
         pl.kp_per_split = 4 * ws * kgs;
@@ -1864,9 +1925,9 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
         if (pl.kp_per_split / 4 / kGemvWaves > kGemvBatch) launch_gemv16_cb<2, true>(p, grid, stream);
         else launch_gemv16_cb<2, false>(p, grid, stream);
     } else if (pl.kind == 6) {
+        p.m_tiles_ = pl.m_tiles;
         const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kG32Threads);
-        if (pl.tile_m == 128) hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel<2>, grid, blk, 0, stream, p);
-        else hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel<1>, grid, blk, 0, stream, p);
+        hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel, grid, blk, 0, stream, p);
     } else if (pl.kind == 3) {
         const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kMmaThreads);
         switch (pl.tile_m) {

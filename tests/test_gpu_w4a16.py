@@ -71,14 +71,16 @@ def test_llama_shapes(llmik, cuda, M, K, N):
                                       # or not a power of two, K beyond the staged row
                                       (1, 512, 128, 16), (1, 256, 64, 8), (1, 384, 32, 96),
                                       (1, 20480, 32, 128),
-                                      # M > 16 32x32 matrix-core GEMM: one and two row halves,
-                                      # partial and several m tiles, one-step K, K splits, waves
-                                      # without steps, groups 32..256
+                                      # M >= 2 16-row matrix-core GEMM (N % 128 != 0): row tiles
+                                      # 1/2/4/8, partial and several m tiles, one-step K
                                       (2, 1024, 128, 32), (17, 512, 192, 64), (33, 2048, 64, 256),
-                                      (100, 384, 128, 128), (200, 256, 64, 32), (7, 32, 64, 32),
-                                      (64, 1024, 128, 128), (65, 4096, 64, 128), (129, 512, 128, 64),
-                                      (48, 14336, 64, 128), (300, 128, 192, 32), (24, 32, 64, 32),
-                                      (127, 2048, 320, 256),
+                                      (200, 256, 64, 32), (7, 32, 64, 32), (65, 4096, 64, 128),
+                                      # M > 16 32x32 matrix-core GEMM (N % 128 == 0): partial and
+                                      # several m tiles, one-step and odd-step K, K splits, K
+                                      # ranges without steps, groups 32..256
+                                      (100, 384, 128, 128), (64, 1024, 128, 128), (65, 4096, 128, 128),
+                                      (129, 512, 128, 64), (48, 14336, 128, 128), (300, 128, 256, 32),
+                                      (24, 32, 128, 32), (40, 96, 128, 32), (127, 2048, 384, 256),
                                       # 2 <= M <= 16 matrix-core GEMV: 32-column tiles, splits,
                                       # a K range that ends inside a batch
                                       (3, 4096, 96, 128), (16, 1056, 32, 32), (9, 7168, 64, 512)])
