@@ -251,6 +251,19 @@ __device__ __forceinline__ u32x4 i4x8b_to_f16(uint32_t w) {
 // made from one dword holds nibble i4_perm(e) (pairs (0,4), (1,5), (2,6), (3,7)).
 __host__ __device__ constexpr int i4_perm(int e) { return (e & 1) ? (e >> 1) + 4 : (e >> 1); }
 
+// Per-wave load context of the MFMA kernel: buffer views of one (batch, kv
+// head) slab of the cache that end at the wave's last token w1, so a tile
+// load past the range returns zeros (those tokens are masked to -inf
+// anyway) and needs no clamping; every load is a lane-constant voffset plus
+// a uniform soffset (t0 * row bytes), so a tile costs no VALU address work.
+// The masks of the code conversions live in VGPRs so that each
+// (word & mask) | bias is one three-operand bit op.
+struct TileCtx {
+    __amdgpu_buffer_rsrc_t rk, rv, rks, rvs, rkg;
+    uint32_t koff, voff, soff, kgoff;
+    uint32_t m_lo, m_hi, e16, e8;
+};
+
 template <KvFormat F>
 struct MfmaTile;
 
@@ -259,27 +272,26 @@ struct MfmaTile;
 template <>
 struct MfmaTile<KvFormat::F16> {
     static constexpr float kPScale = 256.0f;   // p <= 1 -> fp16 p*256 has no subnormals above 2^-32
+    static constexpr uint32_t kRow = kHeadDim * 2;
     u32x4 k[2][4];
     u32x4 v[8];
-    __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
-                                         int g, int c, const uint16_t* /*ksrow*/) {
-        const uint16_t* kp = static_cast<const uint16_t*>(p.k);
-        const uint16_t* vp = static_cast<const uint16_t*>(p.v);
+    // K: lane (g, c) reads row 16 blk + c, channels 32 ks + 8g; V: rows
+    // 8g + e, channels 8c.
+    __device__ __forceinline__ void load(const TileCtx& x, int t0) {
+        const uint32_t so = (uint32_t)t0 * kRow;
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            const long row = row_base + min(t0 + 16 * blk + c, t_last);
+        for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) k[blk][ks] = stream16(kp + row * kHeadDim + 32 * ks + 8 * g);
-        }
+            for (int ks = 0; ks < 4; ++ks)
+                k[blk][ks] = __builtin_amdgcn_raw_buffer_load_b128(
+                    x.rk, (int)x.koff, (int)(so + 16 * kRow * blk + 64 * ks), 2);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const long row = row_base + min(t0 + 8 * g + e, t_last);
-            v[e] = stream16(vp + row * kHeadDim + 8 * c);
-        }
+        for (int e = 0; e < 8; ++e)
+            v[e] = __builtin_amdgcn_raw_buffer_load_b128(x.rv, (int)x.voff, (int)(so + kRow * e), 2);
     }
-    __device__ __forceinline__ f16x8 kop(int blk, int ks) const { return as_f16x8(k[blk][ks]); }
+    __device__ __forceinline__ f16x8 kop(const TileCtx&, int blk, int ks) const { return as_f16x8(k[blk][ks]); }
     // B operand of PV MFMA j: (V[token 8g+2i][8c+j], V[token 8g+2i+1][8c+j]) per dword i.
-    __device__ __forceinline__ f16x8 vop(int j) const {
+    __device__ __forceinline__ f16x8 vop(const TileCtx&, int j) const {
         const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
         uint32_t d[4];
 #pragma unroll
@@ -297,44 +309,51 @@ struct MfmaTile<KvFormat::F16> {
 template <>
 struct MfmaTile<KvFormat::I8> {
     static constexpr float kPScale = 64.0f;    // p * v_scale * 64 <= 516 * 64 < 65504
+    static constexpr uint32_t kRow = kHeadDim;
     u32x4 k[2][2];
     u32x2 v[8];
     uint16_t ks[2], vs[2];
-    __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
-                                         int g, int c, const uint16_t* /*ksrow*/) {
-        const int8_t* kp = static_cast<const int8_t*>(p.k);
-        const int8_t* vp = static_cast<const int8_t*>(p.v);
+    __device__ __forceinline__ void load(const TileCtx& x, int t0) {
+        const uint32_t so = (uint32_t)t0 * kRow;
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
-            const long row = row_base + min(t0 + 16 * blk + c, t_last);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) k[blk][u] = stream16(kp + row * kHeadDim + 64 * u + 16 * g);
-            ks[blk] = p.k_scale[row];
-            vs[blk] = p.v_scale[row];
+            for (int u = 0; u < 2; ++u)
+                k[blk][u] = __builtin_amdgcn_raw_buffer_load_b128(
+                    x.rk, (int)x.koff, (int)(so + 16 * kRow * blk + 64 * u), 2);
+            ks[blk] = __builtin_amdgcn_raw_buffer_load_b16(x.rks, (int)x.soff, (int)(2 * t0 + 32 * blk), 0);
+            vs[blk] = __builtin_amdgcn_raw_buffer_load_b16(x.rvs, (int)x.soff, (int)(2 * t0 + 32 * blk), 0);
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const long row = row_base + min(t0 + 8 * g + e, t_last);
-            v[e] = stream8(vp + row * kHeadDim + 8 * c);
-        }
+        for (int e = 0; e < 8; ++e)
+            v[e] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                x.rv, (int)x.voff, (int)(so + kRow * e), 2));
     }
-    __device__ __forceinline__ f16x8 kop(int blk, int ks_) const {
+    // Four codes of a dword -> exact fp16 pairs: one v_perm_b32 places bytes
+    // (b0, b1) (or (b2, b3)) under the 0x64 exponent bytes of x.e8, giving
+    // 1024 + u; the bias 1152 = 1024 + 128 is then subtracted.
+    __device__ __forceinline__ f16x8 kop(const TileCtx& x, int blk, int ks_) const {
         const u32x4 w = k[blk][ks_ >> 1];
-        const uint32_t w0 = w[(ks_ & 1) * 2], w1 = w[(ks_ & 1) * 2 + 1];
-        uint32_t a, b, c, d;
-        i8x4_to_f16(w0, a, b);
-        i8x4_to_f16(w1, c, d);
-        return as_f16x8(make_u32x4(a, b, c, d));
+        const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+        uint32_t d[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t wi = w[(ks_ & 1) * 2 + i] ^ 0x80808080u;
+            d[2 * i] = __builtin_bit_cast(uint32_t, as_f16x2(perm_b32(x.e8, wi, 0x07010600u)) - bias);
+            d[2 * i + 1] = __builtin_bit_cast(uint32_t, as_f16x2(perm_b32(x.e8, wi, 0x07030602u)) - bias);
+        }
+        return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
     }
-    __device__ __forceinline__ f16x8 vop(int j) const {
+    __device__ __forceinline__ f16x8 vop(const TileCtx& x, int j) const {
         const int byte = j & 3;
         const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
+        const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
         uint32_t d[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t lo = v[2 * i][j >> 2] ^ 0x80808080u;
             const uint32_t hi = v[2 * i + 1][j >> 2] ^ 0x80808080u;
-            d[i] = u8pair_to_f16x2(perm_b32(hi, lo, sel));
+            d[i] = __builtin_bit_cast(uint32_t, as_f16x2(perm_b32(hi, lo, sel) | x.e16) - bias);
         }
         return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
     }
@@ -345,35 +364,43 @@ struct MfmaTile<KvFormat::I8> {
 template <>
 struct MfmaTile<KvFormat::I4> {
     static constexpr float kPScale = 4.0f;     // p * v_scale * 4 <= 9358 * 4 < 65504
+    static constexpr uint32_t kRow = kHeadDim / 2;
     u32x4 k[2];
     uint32_t v[8];
     uint16_t vs[2];
     u32x4 ksc[4];   // K scales of the tile's group, channels 32g..32g+31 (L2-resident)
     int grp;        // the tile's scale group (a 32-token tile lies in one group)
-    __device__ __forceinline__ void load(const AttnParams& p, long row_base, int t0, int t_last,
-                                         int g, int c, const uint16_t* ksrow) {
-        const int8_t* kp = static_cast<const int8_t*>(p.k);
-        const int8_t* vp = static_cast<const int8_t*>(p.v);
-        grp = min(t0, t_last) / p.group_size;
+    __device__ __forceinline__ void load(const TileCtx& x, int t0, int group_size, int t_last) {
+        const uint32_t so = (uint32_t)t0 * kRow;
+        grp = min(t0, t_last) / group_size;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ksc[i] = load16(ksrow + (long)grp * kHeadDim + 8 * i);
+        for (int i = 0; i < 4; ++i)
+            ksc[i] = __builtin_amdgcn_raw_buffer_load_b128(x.rkg, (int)x.kgoff,
+                                                           (int)((uint32_t)grp * kHeadDim * 2 + 16 * i), 0);
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
-            const long row = row_base + min(t0 + 16 * blk + c, t_last);
-            k[blk] = stream16(kp + row * (kHeadDim / 2) + 16 * g);
-            vs[blk] = p.v_scale[row];
+            k[blk] = __builtin_amdgcn_raw_buffer_load_b128(x.rk, (int)x.koff, (int)(so + 16 * kRow * blk), 2);
+            vs[blk] = __builtin_amdgcn_raw_buffer_load_b16(x.rvs, (int)x.soff, (int)(2 * t0 + 32 * blk), 0);
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const long row = row_base + min(t0 + 8 * g + e, t_last);
-            v[e] = stream4(vp + row * (kHeadDim / 2) + 4 * c);
-        }
+        for (int e = 0; e < 8; ++e)
+            v[e] = __builtin_amdgcn_raw_buffer_load_b32(x.rv, (int)x.voff, (int)(so + kRow * e), 2);
     }
-    __device__ __forceinline__ f16x8 kop(int blk, int ks_) const {
-        const uint32_t w = k[blk][ks_];
-        return as_f16x8(i4x8b_to_f16(w ^ 0x88888888u));
+    // Eight codes of a dword -> fp16 pairs (n0,n4), (n1,n5), (n2,n6), (n3,n7), exact.
+    __device__ __forceinline__ f16x8 kop(const TileCtx& x, int blk, int ks_) const {
+        const uint32_t w = k[blk][ks_] ^ 0x88888888u;
+        const uint32_t w8 = w >> 8;
+        const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
+        const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+        const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
+        const f16x2 a = as_f16x2((w & x.m_lo) | x.e16) - bias;
+        const f16x2 b = as_f16x2((w & x.m_hi) | x.e16) * sixteenth - bias16;
+        const f16x2 c = as_f16x2((w8 & x.m_lo) | x.e16) - bias;
+        const f16x2 d = as_f16x2((w8 & x.m_hi) | x.e16) * sixteenth - bias16;
+        return as_f16x8(make_u32x4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                   __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)));
     }
-    __device__ __forceinline__ f16x8 vop(int j) const {
+    __device__ __forceinline__ f16x8 vop(const TileCtx& x, int j) const {
         const int byte = j >> 1;
         const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
         const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
@@ -382,10 +409,10 @@ struct MfmaTile<KvFormat::I4> {
         uint32_t d[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t x = perm_b32(v[2 * i + 1] ^ 0x88888888u, v[2 * i] ^ 0x88888888u, sel);
+            const uint32_t xw = perm_b32(v[2 * i + 1] ^ 0x88888888u, v[2 * i] ^ 0x88888888u, sel);
             f16x2 h;
-            if (j & 1) h = as_f16x2((x & 0x00F000F0u) | 0x64006400u) * sixteenth - bias16;
-            else h = as_f16x2((x & 0x000F000Fu) | 0x64006400u) - bias;
+            if (j & 1) h = as_f16x2((xw & x.m_hi) | x.e16) * sixteenth - bias16;
+            else h = as_f16x2((xw & x.m_lo) | x.e16) - bias;
             d[i] = __builtin_bit_cast(uint32_t, h);
         }
         return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
@@ -459,6 +486,43 @@ void decode_attention_mfma_kernel(AttnParams p) {
         w0 = min(t_begin + wave * per_wave, t_end);
         w1 = min(w0 + per_wave, t_end);
     }
+    // Load context of this wave (buffer views end at its last token w1).
+    TileCtx x;
+    {
+        const long slab = (long)(b * p.n_kv_heads + kvh);
+        constexpr uint32_t kRow = MfmaTile<F>::kRow;
+        const long kv_base = slab * p.kv_buf_len * (long)kRow;
+        const uint32_t range = (uint32_t)max(w1, 0) * kRow;
+        x.rk = make_buffer_rsrc(static_cast<const char*>(p.k) + kv_base, range);
+        x.rv = make_buffer_rsrc(static_cast<const char*>(p.v) + kv_base, range);
+        if constexpr (F != KvFormat::F16) {
+            x.rvs = make_buffer_rsrc(p.v_scale + slab * p.kv_buf_len, (uint32_t)max(w1, 0) * 2u);
+            x.rks = make_buffer_rsrc(F == KvFormat::I8 ? p.k_scale + slab * p.kv_buf_len : p.v_scale,
+                                     (uint32_t)max(w1, 0) * 2u);
+        } else {
+            x.rvs = x.rv;
+            x.rks = x.rk;
+        }
+        x.rkg = (F == KvFormat::I4)
+            ? make_buffer_rsrc(p.k_scale + slab * p.n_groups * kHeadDim, (uint32_t)p.n_groups * kHeadDim * 2u)
+            : x.rk;
+        if constexpr (F == KvFormat::F16) {
+            x.koff = (uint32_t)c * kRow + 16u * g;
+            x.voff = 8u * g * kRow + 16u * c;
+        } else if constexpr (F == KvFormat::I8) {
+            x.koff = (uint32_t)c * kRow + 16u * g;
+            x.voff = 8u * g * kRow + 8u * c;
+        } else {
+            x.koff = (uint32_t)c * kRow + 16u * g;
+            x.voff = 8u * g * kRow + 4u * c;
+        }
+        x.soff = 2u * c;
+        x.kgoff = 64u * g;
+        x.m_lo = vgpr_const(0x000F000Fu);
+        x.m_hi = vgpr_const(0x00F000F0u);
+        x.e16 = vgpr_const(0x64006400u);
+        x.e8 = vgpr_const(0x64646464u);
+    }
     int cur_group = -1;
 
     auto step = [&](const MfmaTile<F>& tile, const int t0) {
@@ -497,7 +561,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const f16x8 kb = tile.kop(blk, ks);
+                const f16x8 kb = tile.kop(x, blk, ks);
                 acc = mfma16x16x32(qa[ks], kb, acc);
                 if constexpr (F == KvFormat::I4) acc = mfma16x16x32(qlo[ks], kb, acc);
             }
@@ -550,12 +614,13 @@ void decode_attention_mfma_kernel(AttnParams p) {
 
         // ---- O += P V ----
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(j), o[j]);
+        for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(x, j), o[j]);
     };
 
-    // K-scale row of this (batch, kv head) for lane group g (INT4 only).
-    const uint16_t* ksrow = (F == KvFormat::I4)
-        ? p.k_scale + (long)(b * p.n_kv_heads + kvh) * p.n_groups * kHeadDim + 32 * g : nullptr;
+    auto load_tile = [&](MfmaTile<F>& t, int t0) {
+        if constexpr (F == KvFormat::I4) t.load(x, t0, p.group_size, w1 - 1);
+        else t.load(x, t0);
+    };
     // The scheduling barriers keep each tile's V loads next to its K loads
     // (the scheduler would otherwise sink them below the QK products, which
     // costs a second memory round trip per tile).
@@ -565,26 +630,26 @@ void decode_attention_mfma_kernel(AttnParams p) {
         // the queue (measured slower for both).
         for (int t0 = w0; t0 < w1; t0 += kWaveStride) {
             MfmaTile<F> tile;
-            tile.load(p, row_base, t0, w1 - 1, g, c, ksrow);
+            load_tile(tile, t0);
             __builtin_amdgcn_sched_barrier(0);
             step(tile, t0);
         }
     } else if (w0 < w1) {
         // INT4 tiles are 4 KiB per wave: the next tile's loads are issued
         // before the current tile's arithmetic. The prefetch is
-        // unconditional (rows past the range clamp to the last row, so it
-        // stays in bounds): a conditional one would make the compiler's wait
-        // count assume it absent and wait for every outstanding load.
+        // unconditional (past the range it reads zeros through the buffer
+        // bound): a conditional one would make the compiler's wait count
+        // assume it absent and wait for every outstanding load.
         MfmaTile<F> ta, tb;
         int t0 = w0;
-        ta.load(p, row_base, t0, w1 - 1, g, c, ksrow);
+        load_tile(ta, t0);
         while (true) {
-            tb.load(p, row_base, t0 + kWaveStride, w1 - 1, g, c, ksrow);
+            load_tile(tb, t0 + kWaveStride);
             __builtin_amdgcn_sched_barrier(0);
             step(ta, t0);
             t0 += kWaveStride;
             if (t0 >= w1) break;
-            ta.load(p, row_base, t0 + kWaveStride, w1 - 1, g, c, ksrow);
+            load_tile(ta, t0 + kWaveStride);
             __builtin_amdgcn_sched_barrier(0);
             step(tb, t0);
             t0 += kWaveStride;
@@ -899,8 +964,11 @@ static int launch_attention(const AttnLaunch& a, hipStream_t stream) {
     p.gqa = a.n_heads / a.n_kv_heads;
     p.scale_log2 = a.softmax_scale * kLog2e;
 
-    // The MFMA path keeps each 32-token tile inside one INT4 K-scale group.
-    const bool mfma = (F != KvFormat::I4) || (p.group_size % kTile == 0);
+    // The MFMA path keeps each 32-token tile inside one INT4 K-scale group,
+    // and addresses a (batch, kv head) slab with 32-bit buffer offsets.
+    const long row_bytes = (F == KvFormat::F16) ? 2 * kHeadDim : (F == KvFormat::I8 ? kHeadDim : kHeadDim / 2);
+    const bool mfma = ((F != KvFormat::I4) || (p.group_size % kTile == 0)) &&
+                      (long)a.kv_buf_len * row_bytes < (1L << 32);
     dim3 grid(pl.n_splits, a.n_kv_heads * pl.n_hchunks, a.batch);
     switch (pl.hpw) {
         case 4: launch_kernel<F, 4>(p, grid, mfma, pl.waves, stream); break;
