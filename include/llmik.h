@@ -231,6 +231,37 @@ LLMIK_API llmik_status llmik_w4a16_dequantize(
     const void* weight_packed, const void* scale, void* out, int K, int N, int group_size,
     void* stream);
 
+/*
+ * Symmetric INT4 group-wise weight quantisation on the GPU, bit-exact to the
+ * reference's host-side torch function.
+ * Replaces: quantize_weights_int4_groupwise (reference/quant_matmul_ref.py:39-88),
+ *   which the reference runs with torch ops when a layer is converted
+ *   (integration/w4a16_patch.py:78-84) and in its tests
+ *   (tests/test_quant.py:265-267).
+ *   W         [K, N] fp16 (w_fp16 != 0) or fp32
+ *   q         [K, N] int8 codes in [-7, 7], or NULL
+ *   packed    [K/8, N] int32 (pack_int4_along_k of q), or NULL; needs K and
+ *             group_size to be multiples of 8
+ *   scale     [ceil(K/group_size), N] in W's dtype, or NULL
+ *   scale_f16 [ceil(K/group_size), N] fp16 (scale rounded to fp16, the
+ *             convention of integration/w4a16_patch.py:84), or NULL
+ * scale = max(absmax_group |W| / 7, 1e-8) evaluated in W's dtype (fp16:
+ * the quotient is rounded to fp16 and the floor is fp16(1e-8) = 0); codes
+ * are clamp(rint(fp32 W / fp32 scale), -7, 7) with true division and
+ * half-to-even rounding, NaN -> 0; a short last group uses its real rows.
+ */
+LLMIK_API llmik_status llmik_quantize_weights_int4_groupwise(
+    const void* W, int w_fp16, int K, int N, int group_size, void* q, void* packed, void* scale,
+    void* scale_f16, void* stream);
+
+/*
+ * Replaces: pack_int4_along_k (reference/quant_matmul_ref.py:140-165).
+ *   q [K, N] int8 -> packed [K/8, N] int32, bits 4i..4i+3 of word (kp, n) =
+ *   q[8 kp + i, n] & 0xF. K must be a multiple of 8.
+ */
+LLMIK_API llmik_status llmik_pack_int4_along_k(const void* q, int K, int N, void* packed,
+                                               void* stream);
+
 /* ------------------------------------------------------ fused elementwise ops */
 
 /*

@@ -321,6 +321,32 @@ LLMIK_API llmik_status llmik_w4a16_dequantize(const void* weight_packed, const v
     return launch_w4a16_dequantize(weight_packed, scale, out, K, N, group_size, as_stream(stream));
 }
 
+LLMIK_API llmik_status llmik_quantize_weights_int4_groupwise(const void* W, int w_fp16, int K, int N,
+                                                             int group_size, void* q, void* packed,
+                                                             void* scale, void* scale_f16,
+                                                             void* stream) {
+    if (K < 0 || N < 0) return invalid("negative dimension");
+    if (group_size <= 0) return invalid("group_size must be positive");
+    if (packed && (K % 8 != 0 || group_size % 8 != 0))
+        return invalid("packing needs K and group_size to be multiples of 8");
+    if ((long)K * N > 0 && !W) return invalid("null pointer");
+    if ((long)K * N >= (1L << 31)) return set_error(LLMIK_ERR_UNSUPPORTED, "W has 2^31 or more elements");
+    if (!aligned(W, w_fp16 ? 2 : 4) || !aligned(scale, w_fp16 ? 2 : 4) || !aligned(scale_f16, 2) ||
+        !aligned(packed, 4))
+        return set_error(LLMIK_ERR_ALIGNMENT, "misaligned buffer");
+    return launch_quantize_weights_int4(W, w_fp16 != 0, K, N, group_size, q, packed, scale, scale_f16,
+                                        as_stream(stream));
+}
+
+LLMIK_API llmik_status llmik_pack_int4_along_k(const void* q, int K, int N, void* packed,
+                                               void* stream) {
+    if (K < 0 || N < 0) return invalid("negative dimension");
+    if (K % 8 != 0) return invalid("K must be a multiple of 8");
+    if ((long)K * N > 0 && (!q || !packed)) return invalid("null pointer");
+    if (!aligned(packed, 4)) return set_error(LLMIK_ERR_ALIGNMENT, "packed must be 4-byte aligned");
+    return launch_pack_int4_along_k(q, K, N, packed, as_stream(stream));
+}
+
 LLMIK_API llmik_status llmik_rmsnorm(const void* x, const void* weight, void* out, int rows,
                                      int hidden, float eps, void* stream) {
     if (rows < 0 || hidden < 0) return invalid("negative dimension");

@@ -95,6 +95,11 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
                  hipStream_t stream);
 int launch_w4a16_dequantize(const void* w, const void* scale, void* out, int K, int N,
                             int group_size, hipStream_t stream);
+// Group-wise INT4 weight quantiser (any of q / packed / scale / scale_f16
+// may be null; packed needs K % 8 == 0 and group_size % 8 == 0).
+int launch_quantize_weights_int4(const void* W, bool w_fp16, int K, int N, int group_size, void* q,
+                                 void* packed, void* scale, void* scale_f16, hipStream_t stream);
+int launch_pack_int4_along_k(const void* q, int K, int N, void* packed, hipStream_t stream);
 
 // ---- fused elementwise -----------------------------------------------------
 int launch_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps,

@@ -18,7 +18,13 @@ the reference):
   * `quantize_per_token_into`, `quantize_v_per_token_int4_into`,
     `quantize_k_per_channel_groupwise_int4_into`: the writers quantising
     into a preallocated cache at a token offset (no torch.cat), used by the
-    cat-free caches in `llmik_cuda.kv_cache`.
+    cat-free caches in `llmik_cuda.kv_cache`;
+  * `quantize_weights_int4_groupwise`, `pack_int4_along_k`: GPU versions of
+    the reference's host-side weight quantiser and packer
+    (reference/quant_matmul_ref.py:39-88, 140-165), same arguments and
+    results bit for bit, and `quantize_pack_weights_int4`, the two fused
+    into the buffers QuantizedLinear registers
+    (integration/w4a16_patch.py:78-84).
 """
 from __future__ import annotations
 
@@ -33,7 +39,8 @@ __all__ = [
     "quantize_k_per_channel_groupwise_int4", "quantize_v_per_token_int4",
     "decode_attention_int4", "w4a16_gemm", "w4a16_dequantize", "rmsnorm", "silu_mul", "rope",
     "w4a16_gemm_f32out", "quantize_per_token_into", "quantize_v_per_token_int4_into",
-    "quantize_k_per_channel_groupwise_int4_into", "LIB_PATH",
+    "quantize_k_per_channel_groupwise_int4_into", "quantize_weights_int4_groupwise",
+    "pack_int4_along_k", "quantize_pack_weights_int4", "LIB_PATH",
 ]
 
 
@@ -437,6 +444,77 @@ def w4a16_dequantize(weight_packed: torch.Tensor, scale: torch.Tensor,
         check(lib.llmik_w4a16_dequantize(_ptr(weight_packed), _ptr(scale), _ptr(out), K, N,
                                          int(group_size), _stream(scale)))
     return out
+
+
+# ------------------------------------------------------ W4 weight quantiser
+
+def _check_weight(W: torch.Tensor, group_size: int) -> Tuple[int, int]:
+    _require(_is_device(W), "W must be a CUDA tensor")
+    _require(W.dtype in (torch.float16, torch.float32), "W must be fp16 or fp32")
+    _require(W.dim() == 2, "W must be 2D [K, N]")
+    _require(W.is_contiguous(), "W must be contiguous")
+    _require(int(group_size) > 0, "group_size must be positive")
+    return int(W.shape[0]), int(W.shape[1])
+
+
+def quantize_weights_int4_groupwise(W: torch.Tensor, group_size: int = 128
+                                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric INT4 group-wise quantisation of W [K, N] (fp16 or fp32) on
+    the GPU: (q [K, N] int8 in [-7, 7], scale [ceil(K/group_size), N] in
+    W's dtype), bit for bit the reference's host-side function
+    (reference/quant_matmul_ref.py:39-88), fp16 and fp32 semantics
+    included."""
+    K, N = _check_weight(W, group_size)
+    g = int(group_size)
+    n_groups = (K + g - 1) // g
+    q = torch.empty((K, N), dtype=torch.int8, device=W.device)
+    scale = torch.empty((n_groups, N), dtype=W.dtype, device=W.device)
+    with torch.cuda.device(W.device):
+        check(lib.llmik_quantize_weights_int4_groupwise(
+            _ptr(W), int(W.dtype == torch.float16), K, N, g, _ptr(q), None, _ptr(scale), None,
+            _stream(W)))
+    return q, scale
+
+
+def pack_int4_along_k(q_int8: torch.Tensor) -> torch.Tensor:
+    """[K, N] int8 -> [K/8, N] int32, bits 4i..4i+3 of word (kp, n) = K
+    position 8 kp + i (reference/quant_matmul_ref.py:140-165), on the GPU."""
+    _require(_is_device(q_int8), "q must be a CUDA tensor")
+    _require(q_int8.dtype == torch.int8 and q_int8.dim() == 2 and q_int8.is_contiguous(),
+             "q must be a contiguous 2D int8 tensor")
+    K, N = q_int8.shape
+    assert K % 8 == 0, f"K={K} must be a multiple of 8 to pack int4 along K"
+    packed = torch.empty((K // 8, N), dtype=torch.int32, device=q_int8.device)
+    with torch.cuda.device(q_int8.device):
+        check(lib.llmik_pack_int4_along_k(_ptr(q_int8), K, N, _ptr(packed), _stream(q_int8)))
+    return packed
+
+
+def quantize_pack_weights_int4(W: torch.Tensor, group_size: int = 128
+                               ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The two buffers QuantizedLinear registers for a [K, N] weight
+    (integration/w4a16_patch.py:78-84): (pack_int4_along_k(q) [K/8, N]
+    int32, scale.to(float16)), with (q, scale) =
+    quantize_weights_int4_groupwise(W, group_size). One kernel when K and
+    group_size are multiples of 8."""
+    K, N = _check_weight(W, group_size)
+    g = int(group_size)
+    assert K % 8 == 0, f"K={K} must be a multiple of 8 to pack int4 along K"
+    n_groups = (K + g - 1) // g
+    packed = torch.empty((K // 8, N), dtype=torch.int32, device=W.device)
+    scale16 = torch.empty((n_groups, N), dtype=torch.float16, device=W.device)
+    with torch.cuda.device(W.device):
+        if g % 8 == 0:
+            check(lib.llmik_quantize_weights_int4_groupwise(
+                _ptr(W), int(W.dtype == torch.float16), K, N, g, None, _ptr(packed), None,
+                _ptr(scale16), _stream(W)))
+        else:
+            q = torch.empty((K, N), dtype=torch.int8, device=W.device)
+            check(lib.llmik_quantize_weights_int4_groupwise(
+                _ptr(W), int(W.dtype == torch.float16), K, N, g, _ptr(q), None, None,
+                _ptr(scale16), _stream(W)))
+            check(lib.llmik_pack_int4_along_k(_ptr(q), K, N, _ptr(packed), _stream(W)))
+    return packed, scale16
 
 
 # --------------------------------------------------------- fused elementwise

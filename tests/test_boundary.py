@@ -95,6 +95,14 @@ def test_c_layer_argument_errors(lib):
     assert st == -1 and "n_groups * group_size" in _err(lib)
     st = lib.llmik_rope(16, 16, 16, 16, 1, 1, 1, 7, S)
     assert st == -1 and "even" in _err(lib)
+    st = lib.llmik_quantize_weights_int4_groupwise(16, 0, 96, 40, 12, None, 16, 16, None, S)
+    assert st == -1 and "multiples of 8" in _err(lib)
+    st = lib.llmik_quantize_weights_int4_groupwise(16, 0, 64, 40, 0, 16, None, 16, None, S)
+    assert st == -1 and "group_size must be positive" in _err(lib)
+    st = lib.llmik_quantize_weights_int4_groupwise(18, 0, 64, 40, 32, 16, None, 16, None, S)
+    assert st == -4
+    st = lib.llmik_pack_int4_along_k(16, 12, 40, 16, S)
+    assert st == -1 and "multiple of 8" in _err(lib)
 
 
 def test_workspace_sizes_without_gpu(lib):
@@ -213,6 +221,25 @@ def test_python_validation_messages(as_device, case):
     _, call, msg = case
     with pytest.raises(RuntimeError, match=msg):
         call(as_device)
+
+
+def test_weight_quantiser_validation(mod, as_device):
+    """The GPU weight quantiser / packer mirror the reference functions'
+    arguments; the packer's K % 8 check is the reference's assertion
+    (reference/quant_matmul_ref.py:157)."""
+    with pytest.raises(RuntimeError, match="W must be fp16 or fp32"):
+        mod.quantize_weights_int4_groupwise(_t(64, 8, dtype=torch.int32), 32)
+    with pytest.raises(RuntimeError, match="group_size must be positive"):
+        mod.quantize_weights_int4_groupwise(_t(64, 8), 0)
+    with pytest.raises(RuntimeError, match=r"W must be 2D \[K, N\]"):
+        mod.quantize_weights_int4_groupwise(_t(64), 32)
+    with pytest.raises(AssertionError, match="K=12 must be a multiple of 8"):
+        mod.pack_int4_along_k(_t(12, 4, dtype=torch.int8))
+    with pytest.raises(AssertionError, match="K=12 must be a multiple of 8"):
+        mod.quantize_pack_weights_int4(_t(12, 4), 4)
+    sig = inspect.signature(mod.quantize_weights_int4_groupwise)
+    assert list(sig.parameters) == ["W", "group_size"] and sig.parameters["group_size"].default == 128
+    assert list(inspect.signature(mod.pack_int4_along_k).parameters) == ["q_int8"]
 
 
 # ------------------------------------------------------- in-place KV writers
