@@ -261,6 +261,43 @@ def bench_writers(llmik, B: int, S: int, steps: int, warmup: int, seed: int = 0)
     return out
 
 
+def bench_wquant(llmik, steps: int, warmup: int, seed: int = 0, gs: int = 128):
+    """The offline weight path: quantize_pack_weights_int4 on an fp32 [K, N]
+    weight (QuantizedLinear's convention), at the three Llama shapes. Bytes:
+    the fp32 weight read once, the packed words and fp16 scales written.
+    Gated bit-for-bit against a torch restatement of the reference's
+    quantiser on the GPU (reference/quant_matmul_ref.py:39-88)."""
+    import torch
+    dev = torch.device("cuda:0")
+    out = []
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
+        nbytes = K * N * 4 + K * N // 2 + (K // gs) * N * 2
+        n_sets = n_sets_for(nbytes)
+        ws = [torch.randn((K, N), generator=gen, device=dev) * 0.02 for _ in range(n_sets)]
+        packed, s16 = llmik.quantize_pack_weights_int4(ws[0], gs)
+        wg = ws[0].view(K // gs, gs, N)
+        # Tensor / tensor: torch's GPU division by a Python scalar multiplies
+        # by the reciprocal, which is not the reference's CPU true division.
+        amax = wg.abs().amax(dim=1)
+        scale = (amax / torch.full_like(amax, 7.0)).clamp(min=1e-8)
+        q = (wg / scale.unsqueeze(1)).round().clamp(-7, 7).to(torch.int64).view(K, N)
+        shifts = torch.arange(8, device=dev, dtype=torch.int64).view(1, 8, 1) * 4
+        ref = ((q.view(K // 8, 8, N) & 0xF) << shifts).sum(dim=1)
+        if not (torch.equal(packed.to(torch.int64) & 0xFFFFFFFF, ref) and
+                torch.equal(s16, scale.half())):
+            raise SystemExit(f"correctness gate failed for w4 quantiser K={K} N={N}")
+        del packed, s16, wg, scale, q, ref
+        fns = [lambda w=w: llmik.quantize_pack_weights_int4(w, gs) for w in ws]
+        us = time_steps(fns, warmup, steps)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append({"name": "w4_quantize_pack_fp32", "K": K, "N": N, "us": round(us, 3),
+                    "bytes": nbytes, "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+        del ws, fns
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_append(llmik, B: int, S: int, steps: int, warmup: int, seed: int = 0):
     """One decode step's KV append at cache length S (B batches, 8 kv heads,
     one new token): the cat-free caches (in-place writers) next to the
@@ -344,10 +381,10 @@ def cpu_baseline(budget_s: float = 15.0):
 
 
 def cpu_details(budget_s: float = 4.0):
-    """The oracle's writers and W4A16 reference matmul (reference forms:
-    quantisers on x.float(), quantized_matmul_ref with its per-call fp32
-    dequant) on the host, one config each, median of the calls that fit in
-    `budget_s` (at least 2)."""
+    """The oracle's writers, W4A16 reference matmul and weight quantiser +
+    packer (reference forms: quantisers on x.float(), quantized_matmul_ref
+    with its per-call fp32 dequant) on the host, one config each, median of
+    the calls that fit in `budget_s` (at least 2)."""
     import numpy as np
     from oracle import kv_quant as okq
     from oracle import w4a16 as ow
@@ -381,6 +418,14 @@ def cpu_details(budget_s: float = 4.0):
         us, n = timed(lambda: ow.quantized_matmul_ref(act, q, s, 128))
         out.append({"name": "w4a16", "M": 1, "K": K, "N": N, "cpu_us": us, "calls": n})
         del q, s
+    W = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+
+    def quant_pack():
+        q, s = ow.quantize_weights_int4_groupwise(W, 128)
+        return ow.pack_int4_along_k(q), s.astype(np.float16)
+    us, n = timed(quant_pack)
+    out.append({"name": "w4_quantize_pack_fp32", "K": 4096, "N": 4096, "cpu_us": us, "calls": n})
+    del W
     return out
 
 
@@ -438,7 +483,7 @@ def main() -> None:
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list: int8,int4,w4a16,writers,append,sweep")
+                    help="comma list: int8,int4,w4a16,writers,append,sweep,wquant")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the counter-collection program (headline calls + copies) and exit")
     args = ap.parse_args()
@@ -488,6 +533,9 @@ def main() -> None:
             log(details[-3:])
         if want("append"):
             details.extend(bench_append(llmik, 8, 4096, 50, 5, seed=8))
+            log(details[-3:])
+        if want("wquant"):
+            details.extend(bench_wquant(llmik, 20, 3, seed=9))
             log(details[-3:])
     gpu_wall = time.perf_counter() - t_wall
 
