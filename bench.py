@@ -5,7 +5,9 @@ Llama-3-8B decode shape B=8, H=32, Hkv=8, D=128, S=4096 — one step is one
 decode_attention call over one batch of synthetic inputs. The other
 BASELINE.json configs (INT8 / INT4 KIVI attention, the KV writers, W4A16 at
 M in {1, 16, 128} on the three Llama shapes, the S / B sweep) are measured
-the same way and reported under "details".
+the same way and reported under "details", beside the wider rows: W4A16 at
+prefill sizes (M in {256, 2048}, next to dequantise + hipBLASLt), the
+in-place quantised KV appends and the GPU weight quantiser.
 
 Method
   * Inputs are generated on the GPU from a seeded generator and are resident
@@ -224,6 +226,40 @@ def bench_w4a16(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int 
             "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "TFLOPs": round(tf, 2), "frac_mfma_fp16_peak": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
             "max_abs_err_f32out": err, "sets": n_sets}
+
+
+def bench_prefill(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int = 128,
+                  seed: int = 0):
+    """Prefill-sized W4A16 (M >= 256): the reference's layer switches to
+    w4a16_dequantize + F.linear at 256 rows (integration/w4a16_patch.py:89-116).
+    Times that path (dequantise into a fresh fp16 [K, N], then torch.matmul,
+    i.e. hipBLASLt) beside w4a16_gemm on the same inputs."""
+    import torch
+    dev = torch.device("cuda:0")
+    kern = bench_w4a16(llmik, M, K, N, steps, warmup, gs, seed)
+    nbytes = w4a16_bytes(M, K, N, gs)
+    n_sets = n_sets_for(nbytes)
+    gen = torch.Generator(device=dev).manual_seed(seed + 1)
+    sets = []
+    for _ in range(n_sets):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), generator=gen, device=dev,
+                          dtype=torch.int32)
+        sc = (torch.rand((K // gs, N), generator=gen, device=dev) * 0.004 + 0.001).half()
+        a = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float16)
+        sets.append((a, w, sc))
+    a0, w0, s0 = sets[0]
+    got = torch.matmul(a0, llmik.w4a16_dequantize(w0, s0, gs))
+    ref = a0.float() @ unpack_w4(w0).float().mul(s0.float().repeat_interleave(gs, dim=0))
+    err = float((got.float() - ref).abs().max())
+    del got, ref
+    fns = [lambda s=s: torch.matmul(s[0], llmik.w4a16_dequantize(s[1], s[2], gs)) for s in sets]
+    us = time_steps(fns, warmup, steps)
+    del sets, fns
+    torch.cuda.empty_cache()
+    kern.update({"name": "w4a16_prefill", "dequant_matmul_us": round(us, 3),
+                 "dequant_matmul_max_abs_err": err,
+                 "dequant_matmul_TFLOPs": round(2.0 * M * K * N / (us * 1e-6) / 1e12, 2)})
+    return kern
 
 
 def unpack_w4(w):
@@ -483,7 +519,7 @@ def main() -> None:
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list: int8,int4,w4a16,writers,append,sweep,wquant")
+                    help="comma list: int8,int4,w4a16,prefill,writers,append,sweep,wquant")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the counter-collection program (headline calls + copies) and exit")
     args = ap.parse_args()
@@ -527,6 +563,11 @@ def main() -> None:
             for M in (1, 16, 128):
                 for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
                     details.append(bench_w4a16(llmik, M, K, N, 100 if M < 128 else 30, 10, seed=6))
+                    log(details[-1])
+        if want("prefill"):
+            for M in (256, 2048):
+                for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
+                    details.append(bench_prefill(llmik, M, K, N, 20, 3, seed=10))
                     log(details[-1])
         if want("writers"):
             details.extend(bench_writers(llmik, 8, 4096, 50, 5, seed=7))

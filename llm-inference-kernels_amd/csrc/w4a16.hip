@@ -45,13 +45,24 @@ struct GemmParams {
 //   u = code + 8 (xor 0x8 per nibble); 0x6400 | u is the fp16 value 1024 + u,
 //   and 0x6400 | (u << 4) is 1024 + 16u; subtracting / rescaling recovers
 //   the code exactly.
-__device__ __forceinline__ void i4x8_to_f16_pairs(uint32_t w, f16x2 out[4]) {
-    w ^= 0x88888888u;
+// The masked nibbles and the exponent bits never overlap, so
+//   ((w ^ 0x88888888) & m) | 0x6400 6400  ==  (w & m) ^ (0x6400 6400 | (0x88888888 & m)),
+// one three-operand bit op per pair when the mask and the xor constant sit
+// in VGPRs (CodeMasks, built once per kernel: vgpr_const is volatile and is
+// never re-materialised).
+struct CodeMasks {
+    uint32_t m_lo, m_hi, x_lo, x_hi;
+};
+__device__ __forceinline__ CodeMasks code_masks() {
+    return {vgpr_const(0x000F000Fu), vgpr_const(0x00F000F0u), vgpr_const(0x64086408u),
+            vgpr_const(0x64806480u)};
+}
+__device__ __forceinline__ void i4x8_to_f16_pairs(uint32_t w, f16x2 out[4], const CodeMasks& k) {
     const uint32_t w8 = w >> 8;
-    const uint32_t a = (w & 0x000F000Fu) | 0x64006400u;
-    const uint32_t b = (w & 0x00F000F0u) | 0x64006400u;
-    const uint32_t c = (w8 & 0x000F000Fu) | 0x64006400u;
-    const uint32_t d = (w8 & 0x00F000F0u) | 0x64006400u;
+    const uint32_t a = (w & k.m_lo) ^ k.x_lo;
+    const uint32_t b = (w & k.m_hi) ^ k.x_hi;
+    const uint32_t c = (w8 & k.m_lo) ^ k.x_lo;
+    const uint32_t d = (w8 & k.m_hi) ^ k.x_hi;
     const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
     const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
     const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
@@ -124,6 +135,7 @@ __global__ __launch_bounds__(kGemmThreads) void w4a16_gemv_kernel(GemmParams p) 
     const int kp_per_group = p.group_size / 8;
 
     float acc[COLS], accg[COLS];
+    const CodeMasks km = code_masks();
 #pragma unroll
     for (int j = 0; j < COLS; ++j) acc[j] = accg[j] = 0.0f;
     int g_cur = kp0 / kp_per_group;
@@ -153,7 +165,7 @@ __global__ __launch_bounds__(kGemmThreads) void w4a16_gemv_kernel(GemmParams p) 
 #pragma unroll
             for (int j = 0; j < COLS; ++j) {
                 f16x2 wp[4];
-                i4x8_to_f16_pairs(wv[j], wp);
+                i4x8_to_f16_pairs(wv[j], wp, km);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) accg[j] = __builtin_amdgcn_fdot2(ap[i], wp[i], accg[j], false);
             }
@@ -861,6 +873,7 @@ __global__ __launch_bounds__(kGemvThreads) void w4a16_gemv16_kernel(GemmParams p
                 n_grp - 1);
 
     f32x4 acc[CB], cg[CB];
+    const CodeMasks km = code_masks();
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
         acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -882,7 +895,7 @@ __global__ __launch_bounds__(kGemvThreads) void w4a16_gemv16_kernel(GemmParams p
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) {
                 f16x2 wp[4];
-                i4x8_to_f16_pairs(word_of<CB>(bt.w[j], cb), wp);
+                i4x8_to_f16_pairs(word_of<CB>(bt.w[j], cb), wp, km);
                 f16x8 bop;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -1073,6 +1086,7 @@ __global__ __launch_bounds__(kMmaThreads) void w4a16_gemm_mfma_kernel(GemmParams
     };
 
     f32x4 acc[RT], cg[RT];
+    const CodeMasks km = code_masks();
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         acc[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1088,7 +1102,7 @@ __global__ __launch_bounds__(kMmaThreads) void w4a16_gemm_mfma_kernel(GemmParams
             const int sl = chunk * KC + j;              // step within the split
             if (sl < nst) {
                 f16x2 wp[4];
-                i4x8_to_f16_pairs(wc.w[j], wp);
+                i4x8_to_f16_pairs(wc.w[j], wp, km);
                 f16x8 bop;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -1313,6 +1327,7 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
     };
 
     f32x16 acc[2][2], cg[2][2];
+    const CodeMasks km = code_masks();
     const f32x16 zero16 = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
                            0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1338,7 +1353,7 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     f16x2 wp[4];
-                    i4x8_to_f16_pairs(t.w[js][kc][j], wp);
+                    i4x8_to_f16_pairs(t.w[js][kc][j], wp, km);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         bop[j][2 * i] = wp[i][0];
