@@ -6,7 +6,8 @@ decode_attention call over one batch of synthetic inputs. The other
 BASELINE.json configs (INT8 / INT4 KIVI attention, the KV writers, W4A16 at
 M in {1, 16, 128} on the three Llama shapes, the S / B sweep) are measured
 the same way and reported under "details", beside the wider rows: W4A16 at
-prefill sizes (M in {256, 2048}, next to dequantise + hipBLASLt), the
+prefill sizes (M in {256, 2048}, next to dequantise + hipBLASLt), a whole
+decode step through four Llama-3-8B layers (eager and graph-replayed), the
 in-place quantised KV appends and the GPU weight quantiser.
 
 Method
@@ -260,6 +261,70 @@ def bench_prefill(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: in
                  "dequant_matmul_max_abs_err": err,
                  "dequant_matmul_TFLOPs": round(2.0 * M * K * N / (us * 1e-6) / 1e12, 2)})
     return kern
+
+
+def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmup: int) -> dict:
+    """A decode step through `n_layers` Llama-3-8B layers (llmik_cuda.decode_layer:
+    rmsnorm, W4A16 q/k/v/o/gate/up/down, rope, fp16 cache write, split-K
+    attention over `ctx` tokens, silu_mul, residual adds), launched eagerly
+    from Python and replayed from one HIP graph. Four layers hold ~950 MB of
+    weights and caches, so the replays read HBM, not the Infinity Cache."""
+    import torch
+    from llmik_cuda.decode_layer import DecodeLayer
+    dev = torch.device("cuda:0")
+    layers = []
+    for i in range(n_layers):
+        layer = DecodeLayer(4096, 32, 8, 14336, B, ctx, device=dev, seed=20 + i)
+        g = torch.Generator(device=dev).manual_seed(40 + i)
+        layer.kbuf.normal_(generator=g)
+        layer.vbuf.normal_(generator=g)
+        layers.append(layer)
+    pos = ctx - 1
+    x = torch.randn((B, 4096), generator=torch.Generator(device=dev).manual_seed(60), device=dev,
+                    dtype=torch.float16)
+
+    def model_step(inp):
+        for layer in layers:
+            inp = layer.step(inp, pos)
+        return inp
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            model_step(x)
+        stream.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            model_step(x)
+        end.record(stream)
+    torch.cuda.synchronize()
+    eager_us = start.elapsed_time(end) * 1000.0 / steps
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(steps):
+            model_step(x)
+    with torch.cuda.stream(stream):
+        graph.replay()
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    graph_us = start.elapsed_time(end) * 1000.0 / steps
+    del graph
+    hidden, kv, inter, gs = 4096, 1024, 14336, 128
+    w_elems = hidden * (2 * hidden + 2 * kv) + 3 * hidden * inter
+    nbytes = w_elems // 2 + 2 * (w_elems // gs) + 2 * 2 * B * 8 * ctx * 128
+    del layers
+    torch.cuda.empty_cache()
+    gbs = nbytes * n_layers / (graph_us * 1e-6) / 1e9
+    return {"name": "decode_layer_step", "layers": n_layers, "B": B, "ctx": ctx,
+            "eager_us_per_layer": round(eager_us / n_layers, 3),
+            "graph_us_per_layer": round(graph_us / n_layers, 3),
+            "bytes_per_layer": nbytes, "graph_GBps": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def unpack_w4(w):
@@ -519,7 +584,7 @@ def main() -> None:
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list: int8,int4,w4a16,prefill,writers,append,sweep,wquant")
+                    help="comma list: int8,int4,w4a16,prefill,layer,writers,append,sweep,wquant")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the counter-collection program (headline calls + copies) and exit")
     args = ap.parse_args()
@@ -569,6 +634,9 @@ def main() -> None:
                 for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
                     details.append(bench_prefill(llmik, M, K, N, 20, 3, seed=10))
                     log(details[-1])
+        if want("layer"):
+            details.append(bench_decode_layer(llmik, 4, 8, 4096, 10, 3))
+            log(details[-1])
         if want("writers"):
             details.extend(bench_writers(llmik, 8, 4096, 50, 5, seed=7))
             log(details[-3:])

@@ -1,0 +1,132 @@
+"""One decoder layer's decode step on llmik ops, and its capture in a HIP graph.
+
+The reference runs a Llama decode step on these ops by patching transformers:
+RMSNorm, SwiGLU and RoPE become `rmsnorm`, `silu_mul` and `rope`
+(integration/prealloc_cache.py:113-144), each new token's K and V are written
+in place into a preallocated `[B, Hkv, max_len, D]` cache whose live prefix
+`decode_attention(q, kbuf, vbuf, scale, seqlen)` reads (:42-110), and the
+projections are W4A16 `QuantizedLinear`s (integration/w4a16_patch.py:67-116).
+`DecodeLayer` is that sequence for one layer, without the model around it:
+
+    n1 = rmsnorm(x);  q, k, v = q_proj(n1), k_proj(n1), v_proj(n1)
+    q, k = rope(q), rope(k);  kbuf[:, :, pos] = k;  vbuf[:, :, pos] = v
+    h = x + o_proj(decode_attention(q, kbuf, vbuf, scale, pos + 1))
+    out = h + down_proj(silu_mul(gate_proj(n2), up_proj(n2))),  n2 = rmsnorm(h)
+
+Every op enqueues on the current stream without a host synchronisation, the
+split-K reductions are deterministic and the per-stream workspace is reused,
+so `capture(x, pos)` records one step in a `torch.cuda.CUDAGraph` whose
+replays reproduce the eager step bit for bit. A graph holds one position (the
+cache slot and the live length are baked into its launches): a serving loop
+captures one graph per position, or per bucket of positions, and replays it.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import decode_attention, quantize_pack_weights_int4, rmsnorm, rope, silu_mul, w4a16_gemm
+
+
+class W4Linear:
+    """A W4A16 projection: an fp32 or fp16 [K, N] weight quantised on the GPU
+    in QuantizedLinear's convention (integration/w4a16_patch.py:78-84: int4
+    codes of the fp32 weight, group-wise fp16 scales), applied with
+    `w4a16_gemm`."""
+
+    def __init__(self, w_kn: torch.Tensor, group_size: int = 128) -> None:
+        self.in_features, self.out_features = w_kn.shape
+        self.group_size = group_size
+        self.weight_packed, self.scale = quantize_pack_weights_int4(w_kn.float().contiguous(), group_size)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        return w4a16_gemm(x, self.weight_packed, self.scale, self.group_size)
+
+
+def rope_tables(max_len: int, head_dim: int, theta: float, device: torch.device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin of the rotary embedding, [max_len, head_dim] fp16, in the
+    half-split layout `rope` rotates (frequencies repeated over both halves)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
+    ang = torch.arange(max_len, dtype=torch.float64)[:, None] * inv_freq[None, :]
+    ang = torch.cat([ang, ang], dim=1)
+    return ang.cos().half().to(device), ang.sin().half().to(device)
+
+
+class DecodeLayer:
+    """A Llama-style layer (GQA attention, SwiGLU MLP, W4A16 projections) with
+    a preallocated fp16 KV cache of `max_len` positions for `batch` sequences.
+
+    `weights` maps q, k, v, o, gate, up, down to [in, out] fp32 matrices and
+    ln1, ln2 to [hidden] fp16 vectors; missing entries are drawn from a seeded
+    generator (N(0, 0.02) matrices, N(1, 0.1) norm weights). Only the packed
+    codes and fp16 scales of the matrices are kept."""
+
+    NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def __init__(self, hidden: int, n_heads: int, n_kv_heads: int, intermediate: int, batch: int,
+                 max_len: int, device: Optional[torch.device] = None, head_dim: int = 128,
+                 group_size: int = 128, eps: float = 1e-5, rope_theta: float = 500000.0,
+                 weights: Optional[Dict[str, torch.Tensor]] = None, seed: int = 0) -> None:
+        if n_heads * head_dim != hidden or n_heads % n_kv_heads != 0:
+            raise RuntimeError("hidden must be n_heads * head_dim and n_heads a multiple of n_kv_heads")
+        dev = torch.device("cuda") if device is None else torch.device(device)
+        self.hidden, self.n_heads, self.n_kv_heads = hidden, n_heads, n_kv_heads
+        self.head_dim, self.intermediate, self.batch, self.max_len = head_dim, intermediate, batch, max_len
+        self.eps = eps
+        self.scale = 1.0 / math.sqrt(head_dim)
+        kv = n_kv_heads * head_dim
+        shapes = {"q": (hidden, hidden), "k": (hidden, kv), "v": (hidden, kv), "o": (hidden, hidden),
+                  "gate": (hidden, intermediate), "up": (hidden, intermediate), "down": (intermediate, hidden)}
+        weights = dict(weights or {})
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        for name in self.NAMES:
+            if name not in weights:
+                weights[name] = torch.randn(shapes[name], generator=gen, device=dev) * 0.02
+        for name in ("ln1", "ln2"):
+            if name not in weights:
+                weights[name] = (1.0 + 0.1 * torch.randn(hidden, generator=gen, device=dev)).half()
+        self.proj = {name: W4Linear(weights.pop(name), group_size) for name in self.NAMES}
+        self.ln1 = weights["ln1"].to(dev, torch.float16).contiguous()
+        self.ln2 = weights["ln2"].to(dev, torch.float16).contiguous()
+        self.cos, self.sin = rope_tables(max_len, head_dim, rope_theta, dev)
+        shape = (batch, n_kv_heads, max_len, head_dim)
+        self.kbuf = torch.zeros(shape, dtype=torch.float16, device=dev)
+        self.vbuf = torch.zeros(shape, dtype=torch.float16, device=dev)
+
+    def step(self, x: torch.Tensor, pos: int) -> torch.Tensor:
+        """One decode step for the token at position `pos` (0-based) of every
+        sequence: x [batch, hidden] fp16 -> [batch, hidden] fp16. Writes the
+        token's K and V at cache slot `pos` and attends over positions
+        0..pos."""
+        if not 0 <= pos < self.max_len:
+            raise RuntimeError(f"position {pos} outside the cache (max_len {self.max_len})")
+        B, H, Hkv, D = self.batch, self.n_heads, self.n_kv_heads, self.head_dim
+        p = self.proj
+        n1 = rmsnorm(x, self.ln1, self.eps)
+        cos, sin = self.cos[pos:pos + 1], self.sin[pos:pos + 1]
+        q = rope(p["q"](n1).view(B, H, 1, D), cos, sin)
+        k = rope(p["k"](n1).view(B, Hkv, 1, D), cos, sin)
+        self.kbuf[:, :, pos:pos + 1].copy_(k)
+        self.vbuf[:, :, pos:pos + 1].copy_(p["v"](n1).view(B, Hkv, 1, D))
+        attn = decode_attention(q.view(B, H, D), self.kbuf, self.vbuf, self.scale, pos + 1)
+        h = x + p["o"](attn.view(B, H * D))
+        n2 = rmsnorm(h, self.ln2, self.eps)
+        return h + p["down"](silu_mul(p["gate"](n2), p["up"](n2)))
+
+    def capture(self, x: torch.Tensor, pos: int, warmup: int = 2) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
+        """Record `step(x, pos)` in a CUDA (HIP) graph. Returns the graph and
+        its output tensor; `graph.replay()` reruns the step on whatever `x`
+        holds then. The warm-up steps on the capture stream set up the
+        module's per-stream workspace before capture."""
+        stream = torch.cuda.Stream(device=x.device)
+        stream.wait_stream(torch.cuda.current_stream(x.device))
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                self.step(x, pos)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = self.step(x, pos)
+        return graph, out

@@ -17,7 +17,7 @@ bit-identical to the reference cache's view after the same appends:
   re-quantises its residual before each attention call; V per token.
 * Int8KVCache: K and V per token (the INT8 path of the reference has no
   cache class; this is its prealloc_cache.PreallocCache layout,
-  integration/prealloc_cache.py:287-323, in INT8).
+  integration/prealloc_cache.py:42-79, in INT8).
 """
 from __future__ import annotations
 

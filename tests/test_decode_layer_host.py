@@ -1,0 +1,32 @@
+"""Host-side pieces of llmik_cuda.decode_layer (no GPU needed)."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import tests.helpers  # noqa: F401  (puts the package on sys.path)
+
+
+def test_rope_tables_are_the_half_split_rotary_angles():
+    from llmik_cuda.decode_layer import rope_tables
+    cos, sin = rope_tables(7, 128, 500000.0, torch.device("cpu"))
+    assert cos.shape == (7, 128) and cos.dtype == torch.float16
+    for pos in (0, 3, 6):
+        for i in (0, 1, 17, 63):
+            ang = pos / (500000.0 ** (2 * i / 128))
+            for col in (i, i + 64):      # both halves carry frequency i
+                assert float(cos[pos, col]) == float(torch.tensor(math.cos(ang)).half())
+                assert float(sin[pos, col]) == float(torch.tensor(math.sin(ang)).half())
+    assert torch.all(cos[0] == 1) and torch.all(sin[0] == 0)
+
+
+def test_layer_shape_validation():
+    from llmik_cuda.decode_layer import DecodeLayer
+    with pytest.raises(RuntimeError, match="hidden must be n_heads"):
+        DecodeLayer(hidden=500, n_heads=4, n_kv_heads=2, intermediate=1024, batch=1, max_len=8,
+                    device="cpu")
+    with pytest.raises(RuntimeError, match="multiple of n_kv_heads"):
+        DecodeLayer(hidden=384, n_heads=3, n_kv_heads=2, intermediate=1024, batch=1, max_len=8,
+                    device="cpu")
