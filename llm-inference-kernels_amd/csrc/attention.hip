@@ -262,6 +262,7 @@ struct TileCtx {
     __amdgpu_buffer_rsrc_t rk, rv, rks, rvs, rkg;
     uint32_t koff, voff, soff, kgoff;
     uint32_t m_lo, m_hi, e16, e8;
+    uint32_t x_lo, x_hi;   // INT4: exponent bits of 0x6400 pairs xor the nibble sign bits
 };
 
 template <KvFormat F>
@@ -344,17 +345,19 @@ struct MfmaTile<KvFormat::I8> {
         }
         return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
     }
+    // B operand of PV MFMA j, biased: (V[8g+2i][8c+j], V[8g+2i+1][8c+j]) as
+    // 1152 + code. One permute places the two code bytes under zero bytes;
+    // xor 0x6480 6480 sets the 0x64 exponents and flips the code's sign bit
+    // (1024 + (code + 128)). The bias is taken out once, at the end, from
+    // the sum of P (kVBias).
+    static constexpr float kVBias[2] = {1152.0f, 1152.0f};
+    static constexpr float kVUnscale[2] = {1.0f, 1.0f};
     __device__ __forceinline__ f16x8 vop(const TileCtx& x, int j) const {
         const int byte = j & 3;
         const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
-        const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
         uint32_t d[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = v[2 * i][j >> 2] ^ 0x80808080u;
-            const uint32_t hi = v[2 * i + 1][j >> 2] ^ 0x80808080u;
-            d[i] = __builtin_bit_cast(uint32_t, as_f16x2(perm_b32(hi, lo, sel) | x.e16) - bias);
-        }
+        for (int i = 0; i < 4; ++i) d[i] = perm_b32(v[2 * i + 1][j >> 2], v[2 * i][j >> 2], sel) ^ 0x64806480u;
         return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
     }
 };
@@ -387,33 +390,35 @@ struct MfmaTile<KvFormat::I4> {
             v[e] = __builtin_amdgcn_raw_buffer_load_b32(x.rv, (int)x.voff, (int)(so + kRow * e), 2);
     }
     // Eight codes of a dword -> fp16 pairs (n0,n4), (n1,n5), (n2,n6), (n3,n7), exact.
+    // (w ^ 0x88888888) & m | 0x6400 6400 == (w & m) ^ x.x_lo / x.x_hi: the
+    // masked nibbles, the sign bits flipped and the exponents never overlap.
     __device__ __forceinline__ f16x8 kop(const TileCtx& x, int blk, int ks_) const {
-        const uint32_t w = k[blk][ks_] ^ 0x88888888u;
+        const uint32_t w = k[blk][ks_];
         const uint32_t w8 = w >> 8;
         const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
         const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
         const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
-        const f16x2 a = as_f16x2((w & x.m_lo) | x.e16) - bias;
-        const f16x2 b = as_f16x2((w & x.m_hi) | x.e16) * sixteenth - bias16;
-        const f16x2 c = as_f16x2((w8 & x.m_lo) | x.e16) - bias;
-        const f16x2 d = as_f16x2((w8 & x.m_hi) | x.e16) * sixteenth - bias16;
+        const f16x2 a = as_f16x2((w & x.m_lo) ^ x.x_lo) - bias;
+        const f16x2 b = as_f16x2((w & x.m_hi) ^ x.x_hi) * sixteenth - bias16;
+        const f16x2 c = as_f16x2((w8 & x.m_lo) ^ x.x_lo) - bias;
+        const f16x2 d = as_f16x2((w8 & x.m_hi) ^ x.x_hi) * sixteenth - bias16;
         return as_f16x8(make_u32x4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
                                    __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)));
     }
+    // B operand of PV MFMA j, biased: even j takes the low nibbles (channel
+    // 8c + j even) as 1024 + (code + 8) = code + 1032, odd j the high nibbles
+    // as 1024 + 16 (code + 8) = 16 code + 1152. The bias and the factor 16
+    // are taken out once, at the end, from the sum of P (kVBias, kVUnscale).
+    static constexpr float kVBias[2] = {1032.0f, 1152.0f};
+    static constexpr float kVUnscale[2] = {1.0f, 0.0625f};
     __device__ __forceinline__ f16x8 vop(const TileCtx& x, int j) const {
         const int byte = j >> 1;
         const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
-        const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
-        const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
-        const f16x2 bias16 = {(f16)72.0f, (f16)72.0f};
         uint32_t d[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t xw = perm_b32(v[2 * i + 1] ^ 0x88888888u, v[2 * i] ^ 0x88888888u, sel);
-            f16x2 h;
-            if (j & 1) h = as_f16x2((xw & x.m_hi) | x.e16) * sixteenth - bias16;
-            else h = as_f16x2((xw & x.m_lo) | x.e16) - bias;
-            d[i] = __builtin_bit_cast(uint32_t, h);
+            const uint32_t xw = perm_b32(v[2 * i + 1], v[2 * i], sel);
+            d[i] = (j & 1) ? ((xw & x.m_hi) ^ x.x_hi) : ((xw & x.m_lo) ^ x.x_lo);
         }
         return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
     }
@@ -464,6 +469,12 @@ void decode_attention_mfma_kernel(AttnParams p) {
     f32x4 o[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // INT8 / INT4: V enters the PV products biased (MfmaTile::vop); sum_p
+    // accumulates the row sums of the same fp16 P operand (one more MFMA
+    // against ones, rescaled with o) so that the bias is removed exactly
+    // once at the end: o_j = (o_j - kVBias * sum_p) * kVUnscale.
+    f32x4 sum_p = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f16x8 ones = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
     float m[4], l[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -522,6 +533,8 @@ void decode_attention_mfma_kernel(AttnParams p) {
         x.m_hi = vgpr_const(0x00F000F0u);
         x.e16 = vgpr_const(0x64006400u);
         x.e8 = vgpr_const(0x64646464u);
+        x.x_lo = vgpr_const(0x64086408u);
+        x.x_hi = vgpr_const(0x64806480u);
     }
     int cur_group = -1;
 
@@ -593,6 +606,10 @@ void decode_attention_mfma_kernel(AttnParams p) {
             for (int j = 0; j < 8; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o[j][i] *= alpha[i];
+            if constexpr (F != KvFormat::F16) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sum_p[i] *= alpha[i];
+            }
         }
 
         // ---- p -> LDS (lane group g writes head g) -> A operand ----
@@ -615,6 +632,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
         // ---- O += P V ----
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(x, j), o[j]);
+        if constexpr (F != KvFormat::F16) sum_p = mfma16x16x32(pa, ones, sum_p);
     };
 
     auto load_tile = [&](MfmaTile<F>& t, int t0) {
@@ -666,6 +684,13 @@ void decode_attention_mfma_kernel(AttnParams p) {
     __shared__ float s_l[NW][HPW];
     __shared__ uint32_t s_last;
     constexpr float kInvP = 1.0f / MfmaTile<F>::kPScale;
+    if constexpr (F != KvFormat::F16) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                o[j][i] = (o[j][i] - MfmaTile<F>::kVBias[j & 1] * sum_p[i]) * MfmaTile<F>::kVUnscale[j & 1];
+    }
     if (g == 0) {
 #pragma unroll
         for (int i = 0; i < HPW; ++i)
