@@ -922,8 +922,15 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
     // sequence to fill the chip use 8-wave workgroups (more loads in flight
     // per CU, one combine output per thread); otherwise 4 waves. Every split
     // gets at least one 32-token tile per wave.
+    // A short sequence that 8-wave splits (one 256-token step each) cannot
+    // spread over the chip runs 4-wave splits instead, as long as that keeps
+    // the combine to at most 8 partials: at B=1, S=1024 the 8 splits took
+    // 6.9 us against 9.0 us for 4; at B=1, S=4096 32 splits took 12.6 us
+    // against 10.4 us for 16 (the combine grows with the split count).
     const long target = (long)kAttnWgsPerCu * cus;
-    pl.waves = (base_wgs < target) ? 8 : 4;
+    const long splits8 = ((long)seqlen + 8 * kTile - 1) / (8 * kTile);
+    const bool short_seq = base_wgs * splits8 < target && 2 * splits8 <= 8;
+    pl.waves = (base_wgs < target && !short_seq) ? 8 : 4;
     const int step = kTile * pl.waves;
     long want = (target + base_wgs - 1) / base_wgs;
     const long max_useful = (seqlen + step - 1) / step;
