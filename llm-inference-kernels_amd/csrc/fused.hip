@@ -56,6 +56,57 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     }
 }
 
+// Rows of up to 256 * 8 * NV fp16 (hidden % 8 == 0): the row and the weight
+// are loaded once into registers, both before the reduction, so the kernel
+// waits on memory once instead of twice.
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_regs_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w,
+                                                           uint16_t* __restrict__ out, int hidden,
+                                                           float eps) {
+    const long row = blockIdx.x;
+    const uint16_t* xr = x + row * hidden;
+    uint16_t* orow = out + row * hidden;
+    u32x4 xv[NV], wv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = (threadIdx.x + 256 * k) * 8;
+        const bool ok = i < hidden;
+        xv[k] = ok ? load16(xr + i) : u32x4{0u, 0u, 0u, 0u};
+        wv[k] = ok ? load16(w + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        float v[8];
+        f16x8_to_f32(xv[k], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+    }
+    ss = row16_sum(ss);
+    __shared__ float s_red[16];
+    if ((threadIdx.x & 15) == 0) s_red[threadIdx.x >> 4] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tot += s_red[r];
+    const float inv = 1.0f / sqrtf(tot / (float)hidden + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = (threadIdx.x + 256 * k) * 8;
+        if (i >= hidden) break;
+        float v[8], g[8];
+        f16x8_to_f32(xv[k], v);
+        f16x8_to_f32(wv[k], g);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = (uint32_t)f2h_bits(v[2 * e] * inv * g[2 * e]) |
+                   ((uint32_t)f2h_bits(v[2 * e + 1] * inv * g[2 * e + 1]) << 16);
+        *reinterpret_cast<u32x4*>(orow + i) = o;
+    }
+}
+
 __device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ g,
@@ -104,9 +155,20 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ 
 int launch_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps,
                    hipStream_t stream) {
     if (rows == 0 || hidden == 0) return LLMIK_OK;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream,
-                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
-                       static_cast<uint16_t*>(out), hidden, eps);
+    const uint16_t* xs = static_cast<const uint16_t*>(x);
+    const uint16_t* ws = static_cast<const uint16_t*>(w);
+    uint16_t* os = static_cast<uint16_t*>(out);
+    if (hidden % 8 == 0 && hidden <= 256 * 8 * 4) {
+        const int nv = (hidden + 256 * 8 - 1) / (256 * 8);
+        if (nv == 1)
+            hipLaunchKernelGGL(rmsnorm_regs_kernel<1>, dim3(rows), dim3(256), 0, stream, xs, ws, os, hidden, eps);
+        else if (nv == 2)
+            hipLaunchKernelGGL(rmsnorm_regs_kernel<2>, dim3(rows), dim3(256), 0, stream, xs, ws, os, hidden, eps);
+        else
+            hipLaunchKernelGGL(rmsnorm_regs_kernel<4>, dim3(rows), dim3(256), 0, stream, xs, ws, os, hidden, eps);
+        return check_launch();
+    }
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, xs, ws, os, hidden, eps);
     return check_launch();
 }
 

@@ -91,6 +91,11 @@ class DecodeLayer:
         self.ln1 = weights["ln1"].to(dev, torch.float16).contiguous()
         self.ln2 = weights["ln2"].to(dev, torch.float16).contiguous()
         self.cos, self.sin = rope_tables(max_len, head_dim, rope_theta, dev)
+        # Per-position tables already broadcast over the batch ([max_len,
+        # batch, D]): rope takes a position's [batch, 1, D] slice as is,
+        # where a [1, D] slice would be expanded by a copy on every call.
+        self.cos_b = self.cos[:, None, :].expand(max_len, batch, head_dim).contiguous()
+        self.sin_b = self.sin[:, None, :].expand(max_len, batch, head_dim).contiguous()
         shape = (batch, n_kv_heads, max_len, head_dim)
         self.kbuf = torch.zeros(shape, dtype=torch.float16, device=dev)
         self.vbuf = torch.zeros(shape, dtype=torch.float16, device=dev)
@@ -105,7 +110,7 @@ class DecodeLayer:
         B, H, Hkv, D = self.batch, self.n_heads, self.n_kv_heads, self.head_dim
         p = self.proj
         n1 = rmsnorm(x, self.ln1, self.eps)
-        cos, sin = self.cos[pos:pos + 1], self.sin[pos:pos + 1]
+        cos, sin = self.cos_b[pos].view(B, 1, D), self.sin_b[pos].view(B, 1, D)
         q = rope(p["q"](n1).view(B, H, 1, D), cos, sin)
         k = rope(p["k"](n1).view(B, Hkv, 1, D), cos, sin)
         self.kbuf[:, :, pos:pos + 1].copy_(k)

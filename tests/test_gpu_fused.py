@@ -23,7 +23,8 @@ def _within_one_rounding(out: torch.Tensor, ref: np.ndarray, slack: float = 1e-6
     assert (np.abs(got - ref) <= ulp + slack * np.abs(ref) + 1e-7).all(), np.abs(got - ref).max()
 
 
-@pytest.mark.parametrize("shape", [(16, 4096), (16, 1024), (1, 4096), (512, 4096), (3, 100)])
+@pytest.mark.parametrize("shape", [(16, 4096), (16, 1024), (1, 4096), (512, 4096), (3, 100),
+                                   (4, 8192), (2, 6144), (2, 8200)])
 def test_rmsnorm(llmik, cuda, shape):
     x = randn(shape, 1).astype(np.float16)
     w = randn((shape[-1],), 2).astype(np.float16)
