@@ -251,6 +251,12 @@ __device__ __forceinline__ u32x4 i4x8b_to_f16(uint32_t w) {
 // made from one dword holds nibble i4_perm(e) (pairs (0,4), (1,5), (2,6), (3,7)).
 __host__ __device__ constexpr int i4_perm(int e) { return (e & 1) ? (e >> 1) + 4 : (e >> 1); }
 
+// Eight fp16 in channel order 0..7 -> the order i4_perm (0, 4, 1, 5, 2, 6, 3, 7).
+__device__ __forceinline__ u32x4 i4_pair_order(const u32x4 a) {
+    return make_u32x4(perm_b32(a[2], a[0], 0x05040100u), perm_b32(a[2], a[0], 0x07060302u),
+                      perm_b32(a[3], a[1], 0x05040100u), perm_b32(a[3], a[1], 0x07060302u));
+}
+
 // Per-wave load context of the MFMA kernel: buffer views of one (batch, kv
 // head) slab of the cache that end at the wave's last token w1, so a tile
 // load past the range returns zeros (those tokens are masked to -inf
@@ -448,7 +454,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
 
     // Q as the A operand (4 k-steps); for INT4 the hi/lo pair of q * k_scale.
     f16x8 qa[4], qlo[4];
-    float qf[32];   // INT4 only: q in fp32 for this lane's 32 channels 32g..32g+31
+    f16x8 qp[4];    // INT4 only: q of channels 32g + 8ks + i4_perm(e), the K operand's order
     if constexpr (F == KvFormat::F16) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qa[ks] = as_f16x8(load16(qrow + 32 * ks + 8 * g));
@@ -458,12 +464,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
             qa[ks] = as_f16x8(load16(qrow + 64 * (ks >> 1) + 16 * g + 8 * (ks & 1)));
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float t[8];
-            f16x8_to_f32(load16(qrow + 32 * g + 8 * i), t);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qf[8 * i + e] = t[e];
-        }
+        for (int ks = 0; ks < 4; ++ks) qp[ks] = as_f16x8(i4_pair_order(load16(qrow + 32 * g + 8 * ks)));
     }
 
     f32x4 o[8];
@@ -545,27 +546,15 @@ void decode_attention_mfma_kernel(AttnParams p) {
         if constexpr (F == KvFormat::I4) {
             if (tile.grp != cur_group) {   // wave-uniform; the scales came with the tile
                 cur_group = tile.grp;
-                float sc[32];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float t[8];
-                    f16x8_to_f32(tile.ksc[i], t);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) sc[8 * i + e] = t[e];
-                }
+                // q * s as an fp16 hi + lo pair: an fp16 multiply rounds the
+                // exact product once (hi), and an fp16 fma rounds the exact
+                // q * s - hi once (lo) -- two packed ops per channel pair.
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
-                    f16x8 hi, lo;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int ch = 8 * ks + i4_perm(e);
-                        const float x = qf[ch] * sc[ch];
-                        const f16 xh = (f16)x;
-                        hi[e] = xh;
-                        lo[e] = (f16)(x - (float)xh);
-                    }
+                    const f16x8 sc = as_f16x8(i4_pair_order(tile.ksc[ks]));
+                    const f16x8 hi = qp[ks] * sc;
                     qa[ks] = hi;
-                    qlo[ks] = lo;
+                    qlo[ks] = __builtin_elementwise_fma(qp[ks], sc, -hi);
                 }
             }
         }
