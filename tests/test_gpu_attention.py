@@ -116,7 +116,9 @@ def test_int8_live_length(llmik, cuda):
 
 
 @pytest.mark.parametrize("B,L,gs", [(1, 128, 32), (4, 1000, 32), (8, 4096, 128), (2, 100, 128),
-                                    (8, 2048, 32), (1, 300, 64)])
+                                    (8, 2048, 32), (1, 300, 64),
+                                    # groups that are not multiples of 32: the VALU kernel
+                                    (2, 300, 16), (3, 500, 48), (1, 200, 100)])
 def test_int4_pipeline_matches_oracle(llmik, cuda, B, L, gs):
     q, k, v = _inputs(B, 32, 8, L, seed=7 * L + gs, outliers=True)
     kq_, ks = llmik.quantize_k_per_channel_groupwise_int4(_dev(k, cuda), gs)
