@@ -42,3 +42,38 @@ def test_rope_identity_and_torch():
     rot = torch.cat((-xt[..., 4:], xt[..., :4]), dim=-1)
     ref = xt * torch.from_numpy(c).float()[:, None] + rot * torch.from_numpy(s).float()[:, None]
     assert np.abs(of.rope(x, c, s) - ref.numpy()).max() < 1e-6
+
+
+def test_rope_is_the_stated_plane_rotation():
+    """rope rotates each (i, i + D/2) plane by the angle whose cos / sin it
+    is given, in the direction the reference states for its kernel
+    (kernels/fused/fused_ops.cu:65: rotate_half(x) = [-x[D/2:], x[:D/2]]):
+    e_i -> cos e_i + sin e_{i+D/2} and e_{i+D/2} -> cos e_{i+D/2} - sin e_i.
+    A rotation by theta then -theta is the identity, and two rotations add
+    their angles: a wrong pairing, sign or half fails one of these."""
+    D, h = 8, 4
+    th = np.array([0.3, -1.1, 2.0, 0.7], dtype=np.float64)
+    ang = np.concatenate([th, th])                    # duplicated-frequency layout
+
+    def cs(a):
+        return (np.cos(a)[None, None, :].astype(np.float32), np.sin(a)[None, None, :].astype(np.float32))
+
+    c, s = cs(ang)
+    for i in range(h):
+        e = np.zeros((1, 1, 1, D), np.float32)
+        e[..., i] = 1.0
+        out = of.rope(e, c, s)[0, 0, 0]
+        want = np.zeros(D)
+        want[i], want[i + h] = np.cos(th[i]), np.sin(th[i])
+        assert np.allclose(out, want, atol=1e-6)
+        e = np.zeros((1, 1, 1, D), np.float32)
+        e[..., i + h] = 1.0
+        out = of.rope(e, c, s)[0, 0, 0]
+        want = np.zeros(D)
+        want[i + h], want[i] = np.cos(th[i]), -np.sin(th[i])
+        assert np.allclose(out, want, atol=1e-6)
+    x = randn((1, 1, 1, D), 9)
+    cm, sm = cs(-ang)
+    assert np.allclose(of.rope(of.rope(x, c, s), cm, sm), x, atol=1e-6)
+    c2, s2 = cs(2 * ang)
+    assert np.allclose(of.rope(of.rope(x, c, s), c, s), of.rope(x, c2, s2), atol=1e-5)
