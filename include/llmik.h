@@ -192,6 +192,24 @@ LLMIK_API llmik_status llmik_quantize_k_per_channel_groupwise_int4_into(
     const void* x, int x_len, void* q_cache, void* scale_cache, int batch, int n_kv_heads,
     int n_tok, int head_dim, int cache_len, int offset, int group_size, void* stream);
 
+/* One decode-step token appended to a KIVI INT4 cache in one launch: the
+ * three launches of Int4KIVICache.append for one token (V per token at
+ * position `length`; K into the open group's fp16 tokens and the open group
+ * re-quantised into its codes and scale slot), the same stored bits.
+ * Replaces, for one token, the reference's per-append re-quantise and
+ * torch.cat (integration/kv_int4_cache.py:104-144,168-206).
+ *   k, v     [batch, n_kv_heads, k_len / v_len, 128] fp16; token 0 is appended
+ *   k_open   [batch, n_kv_heads, group_size, 128] fp16: the open group's tokens
+ *            0 .. length % group_size - 1; the new token is written after them
+ *   k_q, v_q [batch, n_kv_heads, max_len, 64] packed int4
+ *   k_scale  [batch, n_kv_heads, ceil(max_len / group_size), 128] fp16
+ *   v_scale  [batch, n_kv_heads, max_len] fp16
+ * group_size <= 128; length < max_len. */
+LLMIK_API llmik_status llmik_kivi_append_token_int4(
+    const void* k, int k_len, const void* v, int v_len, void* k_open, void* k_q, void* k_scale, void* v_q,
+    void* v_scale, int batch, int n_kv_heads, int head_dim, int max_len, int group_size, int length,
+    void* stream);
+
 /* -------------------------------------------------------------------- W4A16
  * out[M, N] = act[M, K] @ dequant(W)[K, N], W[k, n] = q[k, n] * scale[k/g, n],
  * fp32 accumulation.

@@ -266,6 +266,27 @@ LLMIK_API llmik_status llmik_quantize_k_per_channel_groupwise_int4_into(
                                             as_stream(stream));
 }
 
+LLMIK_API llmik_status llmik_kivi_append_token_int4(
+    const void* k, int k_len, const void* v, int v_len, void* k_open, void* k_q, void* k_scale, void* v_q,
+    void* v_scale, int batch, int n_kv_heads, int head_dim, int max_len, int group_size, int length,
+    void* stream) {
+    if (batch < 0 || n_kv_heads < 0 || k_len < 1 || v_len < 1 || max_len < 0)
+        return invalid("negative dimension");
+    if (head_dim != 128) return invalid("only head_dim=128 supported");
+    if (group_size <= 0 || group_size > 128) return invalid("group_size must be in 1..128");
+    if (length < 0 || length >= max_len) return invalid("the cache is full");
+    if ((long)batch * n_kv_heads > 65535L) return invalid("batch * n_kv_heads exceeds 65535");
+    if ((long)batch * n_kv_heads > 0 && (!k || !v || !k_open || !k_q || !k_scale || !v_q || !v_scale))
+        return invalid("null pointer");
+    if (!aligned(k, 16) || !aligned(v, 16) || !aligned(k_open, 16) || !aligned(k_q, 4) ||
+        !aligned(v_q, 4) || !aligned(k_scale, 2) || !aligned(v_scale, 2))
+        return set_error(LLMIK_ERR_ALIGNMENT, "k, v and k_open must be 16-byte aligned");
+    const int n_groups = (max_len + group_size - 1) / group_size;
+    return launch_kivi_append_token(k, (long)k_len * 128, v, (long)v_len * 128, k_open, k_q, k_scale, v_q,
+                                    v_scale, batch * n_kv_heads, length % group_size, length, group_size,
+                                    max_len, n_groups, as_stream(stream));
+}
+
 namespace {
 int check_gemm(const void* act, const void* w, const void* scale, const void* out, int M, int N,
                int K, int group_size) {

@@ -18,6 +18,8 @@
 // dst_off is a multiple of group_size and group g goes to scale slot
 // dst_off / group_size + g). The out-of-place ops are the identity map
 // src_len = dst_len = n_tok, dst_off = 0.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "llmik_internal.hpp"
 
@@ -285,6 +287,125 @@ int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int ro
         hipLaunchKernelGGL(quantize_k_groupwise_int4_kernel<8>, grid, blk, 0, stream, xp, qp, sp, group_size, map, dst_groups);
     else
         hipLaunchKernelGGL(quantize_k_groupwise_int4_large_kernel, grid, blk, 0, stream, xp, qp, sp, group_size, map, dst_groups);
+    return check_launch();
+}
+
+// One decode-step token appended to a KIVI INT4 cache in one launch, per
+// (batch, kv_head) row (one workgroup each; the three launches of the
+// general path, integration/kv_int4_cache.py:104-144 restated in place):
+//   * V: the token quantised per token into v_q / v_scale at position pos;
+//   * K: the token written after the open group's r fp16 tokens (k_open),
+//     and the open group (tokens pos - r .. pos) re-quantised per channel
+//     into its codes and its scale slot (pos - r) / group_size.
+// The arithmetic is the per-token and group-wise writers' above, so the
+// stored codes and scales are the same bits. group_size <= 16 * TPR.
+template <int TPR>
+__global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
+    const uint16_t* __restrict__ k_in, long k_stride, const uint16_t* __restrict__ v_in, long v_stride,
+    uint16_t* __restrict__ k_open, int8_t* __restrict__ k_q, uint16_t* __restrict__ k_scale,
+    int8_t* __restrict__ v_q, uint16_t* __restrict__ v_scale, int r, int pos, int group_size,
+    int max_len, int n_groups) {
+    const long bh = blockIdx.x;
+    const int row = threadIdx.x >> 4;
+    const int c = threadIdx.x & 15;
+    const uint16_t* kin = k_in + bh * k_stride + 8 * c;
+    uint16_t* kopen = k_open + bh * (long)group_size * 128 + 8 * c;
+
+    // ---- K: tokens 0..r of the open group (r from k_in, the rest from k_open)
+    const u32x4 knew = load16(kin);
+    u32x4 raw[TPR];
+#pragma unroll
+    for (int i = 0; i < TPR; ++i) {
+        const int t = min(row + 16 * i, r);   // past the group: a duplicate, which does not move the max
+        raw[i] = (t == r) ? knew : load16(kopen + (long)t * 128);
+    }
+    if (row == (r & 15)) *reinterpret_cast<u32x4*>(kopen + (long)r * 128) = knew;
+
+    float amax[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TPR; ++i) {
+        float xf[8];
+        f16x8_to_f32(raw[i], xf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax[e] = fmaxf(amax[e], fabsf(xf[e]));
+    }
+    __shared__ float s_max[16][128];
+    __shared__ float s_scale[128];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_max[row][8 * c + e] = amax[e];
+    __syncthreads();
+    const int start = pos - r;
+    if (threadIdx.x < 128) {
+        float m = 0.0f;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) m = fmaxf(m, s_max[rr][threadIdx.x]);
+        const float sc = fmaxf(m / 7.0f, 1.0e-8f);
+        s_scale[threadIdx.x] = sc;
+        k_scale[(bh * n_groups + start / group_size) * 128 + threadIdx.x] = f2h_bits(sc);
+    }
+    __syncthreads();
+    float sv[8], rcp[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        sv[e] = s_scale[8 * c + e];
+        rcp[e] = 1.0f / sv[e];
+    }
+#pragma unroll
+    for (int i = 0; i < TPR; ++i) {
+        const int t = row + 16 * i;
+        float xf[8];
+        f16x8_to_f32(raw[i], xf);
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = quant_round(xf[e], sv[e], rcp[e]);
+            v = fminf(fmaxf(v, -7.0f), 7.0f);
+            w |= (uint32_t)((int)v & 0xF) << (4 * e);
+        }
+        if (t <= r) *reinterpret_cast<uint32_t*>(k_q + (bh * max_len + start + t) * 64 + 4 * c) = w;
+    }
+
+    // ---- V: the token per token (row 0's 16 lanes)
+    if (row == 0) {
+        float xf[8];
+        f16x8_to_f32(load16(v_in + bh * v_stride + 8 * c), xf);
+        float amax1 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax1 = fmaxf(amax1, fabsf(xf[e]));
+        amax1 = row16_max(amax1);
+        const float sc = fmaxf(amax1 / 7.0f, 1.0e-8f);
+        const float rc = 1.0f / sc;
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = quant_round(xf[e], sc, rc);
+            v = fminf(fmaxf(v, -7.0f), 7.0f);
+            w |= (uint32_t)((int)v & 0xF) << (4 * e);
+        }
+        *reinterpret_cast<uint32_t*>(v_q + (bh * max_len + pos) * 64 + 4 * c) = w;
+        if (c == 0) v_scale[bh * max_len + pos] = f2h_bits(sc);
+    }
+}
+
+int launch_kivi_append_token(const void* k, long k_stride, const void* v, long v_stride, void* k_open,
+                             void* k_q, void* k_scale, void* v_q, void* v_scale, int rows, int r,
+                             int pos, int group_size, int max_len, int n_groups, hipStream_t stream) {
+    if (rows == 0) return LLMIK_OK;
+    const int tpr = (group_size + 15) / 16;
+    auto go = [&](auto tag) {
+        constexpr int T = decltype(tag)::value;
+        hipLaunchKernelGGL((kivi_append_token_kernel<T>), dim3(rows), dim3(kWriterThreads), 0, stream,
+                           static_cast<const uint16_t*>(k), k_stride, static_cast<const uint16_t*>(v),
+                           v_stride, static_cast<uint16_t*>(k_open), static_cast<int8_t*>(k_q),
+                           static_cast<uint16_t*>(k_scale), static_cast<int8_t*>(v_q),
+                           static_cast<uint16_t*>(v_scale), r, pos, group_size, max_len, n_groups);
+    };
+    if (tpr <= 1) go(std::integral_constant<int, 1>{});
+    else if (tpr <= 2) go(std::integral_constant<int, 2>{});
+    else if (tpr <= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
     return check_launch();
 }
 

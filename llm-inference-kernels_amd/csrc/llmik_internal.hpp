@@ -69,6 +69,9 @@ int launch_quantize_per_token(const void* x, void* q, void* scale, int rows, int
 int launch_quantize_k_groupwise_int4(const void* x, void* q, void* scale, int rows, int n_tok,
                                      int src_len, int dst_len, int dst_off, int dst_groups,
                                      int group_size, hipStream_t stream);
+int launch_kivi_append_token(const void* k, long k_stride, const void* v, long v_stride, void* k_open,
+                             void* k_q, void* k_scale, void* v_q, void* v_scale, int rows, int r,
+                             int pos, int group_size, int max_len, int n_groups, hipStream_t stream);
 
 // ---- W4A16 -----------------------------------------------------------------
 struct GemmPlan {

@@ -40,7 +40,7 @@ __all__ = [
     "decode_attention_int4", "w4a16_gemm", "w4a16_dequantize", "rmsnorm", "silu_mul", "rope",
     "w4a16_gemm_f32out", "quantize_per_token_into", "quantize_v_per_token_int4_into",
     "quantize_k_per_channel_groupwise_int4_into", "quantize_weights_int4_groupwise",
-    "pack_int4_along_k", "quantize_pack_weights_int4", "LIB_PATH",
+    "pack_int4_along_k", "quantize_pack_weights_int4", "kivi_append_token_int4", "LIB_PATH",
 ]
 
 
@@ -348,6 +348,41 @@ def quantize_v_per_token_int4_into(x: torch.Tensor, q_cache: torch.Tensor,
         check(lib.llmik_quantize_v_per_token_int4_into(
             _ptr(x), x_len, _ptr(q_cache), _ptr(scale_cache), batch, n_kv_heads, n_tok, head_dim,
             cache_len, int(offset), _stream(x)))
+
+
+def kivi_append_token_int4(k: torch.Tensor, v: torch.Tensor, k_open: torch.Tensor,
+                           k_q: torch.Tensor, k_scale: torch.Tensor, v_q: torch.Tensor,
+                           v_scale: torch.Tensor, length: int, group_size: int) -> None:
+    """Append token 0 of k, v [batch, n_kv_heads, n, 128] fp16 to a KIVI INT4
+    cache holding `length` tokens, in one launch: V per token at position
+    `length`; K after the open group's fp16 tokens in k_open [batch,
+    n_kv_heads, group_size, 128], the open group re-quantised into k_q /
+    k_scale. Bit-equal to the writers' path (llmik_cuda.kv_cache)."""
+    _require(all(_is_device(t) for t in (k, v, k_open, k_q, k_scale, v_q, v_scale)),
+             "all inputs must be CUDA tensors")
+    _require(k.dtype == torch.float16 and v.dtype == torch.float16 and k_open.dtype == torch.float16,
+             "k, v and k_open must be fp16")
+    _require(k.dim() == 4 and k.shape[:2] == v.shape[:2] and k.size(3) == 128 and v.size(3) == 128,
+             "k and v must be [batch, n_kv_heads, n, 128]")
+    batch, n_kv_heads = k.size(0), k.size(1)
+    max_len = k_q.size(2)
+    n_groups = (max_len + group_size - 1) // group_size
+    _require(tuple(k_q.shape) == (batch, n_kv_heads, max_len, 64) and k_q.shape == v_q.shape
+             and k_q.dtype == torch.int8 and v_q.dtype == torch.int8,
+             "k_q / v_q must be [batch, n_kv_heads, max_len, 64] int8")
+    _require(tuple(k_scale.shape) == (batch, n_kv_heads, n_groups, 128)
+             and tuple(v_scale.shape) == (batch, n_kv_heads, max_len)
+             and k_scale.dtype == torch.float16 and v_scale.dtype == torch.float16,
+             "k_scale / v_scale must be fp16 and match the cache's shape")
+    _require(tuple(k_open.shape) == (batch, n_kv_heads, group_size, 128),
+             "k_open must be [batch, n_kv_heads, group_size, 128]")
+    _require(all(t.is_contiguous() for t in (k_open, k_q, k_scale, v_q, v_scale)),
+             "cache tensors must be contiguous")
+    with torch.cuda.device(k.device):
+        check(lib.llmik_kivi_append_token_int4(
+            _ptr(k), _token_rows(k), _ptr(v), _token_rows(v), _ptr(k_open), _ptr(k_q), _ptr(k_scale),
+            _ptr(v_q), _ptr(v_scale), batch, n_kv_heads, 128, max_len, int(group_size), int(length),
+            _stream(k)))
 
 
 def quantize_k_per_channel_groupwise_int4_into(x: torch.Tensor, q_cache: torch.Tensor,

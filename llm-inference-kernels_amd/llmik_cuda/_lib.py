@@ -43,6 +43,8 @@ _SIGNATURES = {
     "llmik_quantize_v_per_token_int4_into": (_i, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "llmik_quantize_k_per_channel_groupwise_int4_into": (
         _i, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p]),
+    "llmik_kivi_append_token_int4": (
+        _i, [_p, _i, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "llmik_w4a16_workspace_size": (_sz, [_i, _i, _i, _i]),
     "llmik_w4a16_gemm": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
     "llmik_w4a16_gemm_f32out": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),

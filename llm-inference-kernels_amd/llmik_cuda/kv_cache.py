@@ -25,7 +25,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from . import (decode_attention_int4, decode_attention_int8,
+from . import (decode_attention_int4, decode_attention_int8, kivi_append_token_int4,
                quantize_k_per_channel_groupwise_int4_into, quantize_per_token_into,
                quantize_v_per_token_int4_into)
 
@@ -119,6 +119,13 @@ class Int4KIVICache:
         if n == 0:
             return
         g = self.group_size
+        if n == 1 and g <= 128 and self.head_dim == 128:
+            # A decode step: one launch for the V token, the open group's new
+            # fp16 token and its re-quantisation.
+            kivi_append_token_int4(k, v, self.k_open, self.k_q, self.k_scale, self.v_q, self.v_scale,
+                                   self.length, g)
+            self.length += 1
+            return
         quantize_v_per_token_int4_into(v, self.v_q, self.v_scale, self.length)
         pos = 0
         r = self.length % g

@@ -103,6 +103,13 @@ def test_c_layer_argument_errors(lib):
     assert st == -4
     st = lib.llmik_pack_int4_along_k(16, 12, 40, 16, S)
     assert st == -1 and "multiple of 8" in _err(lib)
+    kivi = (16, 1, 16, 1, 16, 16, 16, 16, 16, 1, 8)    # k .. v_scale, batch, n_kv_heads
+    st = lib.llmik_kivi_append_token_int4(*kivi, 128, 64, 32, 64, S)
+    assert st == -1 and "full" in _err(lib)
+    st = lib.llmik_kivi_append_token_int4(*kivi, 128, 512, 256, 64, S)
+    assert st == -1 and "1..128" in _err(lib)
+    st = lib.llmik_kivi_append_token_int4(*kivi, 64, 64, 32, 0, S)
+    assert st == -1 and "head_dim=128" in _err(lib)
 
 
 def test_workspace_sizes_without_gpu(lib):

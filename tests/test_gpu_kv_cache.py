@@ -114,6 +114,8 @@ def _reference_kivi_view(k_all, v_all, g):
     (32, [100, 1, 1, 30, 1, 64, 3]),        # prefill with a partial group, then mixed appends
     (128, [128, 5, 123, 1, 300]),           # KIVI at group 128
     (16, [7, 9, 16, 1, 48]),
+    (64, [1] * 70),                         # single tokens through a whole group of 64
+    (100, [50] + [1] * 60),                 # a group size that is no power of two
 ])
 def test_int4_cache_matches_reference_semantics(llmik, cuda, g, appends):
     from llmik_cuda.kv_cache import Int4KIVICache
