@@ -263,18 +263,20 @@ def bench_prefill(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: in
     return kern
 
 
-def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmup: int) -> dict:
+def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmup: int,
+                       fused: bool = True) -> dict:
     """A decode step through `n_layers` Llama-3-8B layers (llmik_cuda.decode_layer:
     rmsnorm, W4A16 q/k/v/o/gate/up/down, rope, fp16 cache write, split-K
     attention over `ctx` tokens, silu_mul, residual adds), launched eagerly
-    from Python and replayed from one HIP graph. Four layers hold ~950 MB of
+    from Python and replayed from one HIP graph; `fused` picks the merged
+    10-launch step or the op-by-op 17-launch one. Four layers hold ~950 MB of
     weights and caches, so the replays read HBM, not the Infinity Cache."""
     import torch
     from llmik_cuda.decode_layer import DecodeLayer
     dev = torch.device("cuda:0")
     layers = []
     for i in range(n_layers):
-        layer = DecodeLayer(4096, 32, 8, 14336, B, ctx, device=dev, seed=20 + i)
+        layer = DecodeLayer(4096, 32, 8, 14336, B, ctx, device=dev, seed=20 + i, fused=fused)
         g = torch.Generator(device=dev).manual_seed(40 + i)
         layer.kbuf.normal_(generator=g)
         layer.vbuf.normal_(generator=g)
@@ -320,7 +322,8 @@ def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmu
     del layers
     torch.cuda.empty_cache()
     gbs = nbytes * n_layers / (graph_us * 1e-6) / 1e9
-    return {"name": "decode_layer_step", "layers": n_layers, "B": B, "ctx": ctx,
+    return {"name": "decode_layer_step" if fused else "decode_layer_step_op_by_op",
+            "layers": n_layers, "B": B, "ctx": ctx,
             "eager_us_per_layer": round(eager_us / n_layers, 3),
             "graph_us_per_layer": round(graph_us / n_layers, 3),
             "bytes_per_layer": nbytes, "graph_GBps": round(gbs, 1),
@@ -636,7 +639,8 @@ def main() -> None:
                     log(details[-1])
         if want("layer"):
             details.append(bench_decode_layer(llmik, 4, 8, 4096, 10, 3))
-            log(details[-1])
+            details.append(bench_decode_layer(llmik, 4, 8, 4096, 10, 3, fused=False))
+            log(details[-2:])
         if want("writers"):
             details.extend(bench_writers(llmik, 8, 4096, 50, 5, seed=7))
             log(details[-3:])

@@ -306,6 +306,46 @@ LLMIK_API llmik_status llmik_silu_mul(const void* gate, const void* up, void* ou
 LLMIK_API llmik_status llmik_rope(const void* x, const void* cos, const void* sin, void* out,
                                   int B, int H, int S, int D, void* stream);
 
+/* --------------------------------------------------- decode-step merged ops
+ * Consecutive ops of the reference's patched decode step
+ * (integration/prealloc_cache.py:61-76,113-144: the in-place cache write,
+ * RMSNorm, SwiGLU, RoPE) merged into one launch each. Each computes what the ops it
+ * replaces compute, with the same roundings; no single reference function
+ * corresponds to them. */
+
+/*
+ * qkv [batch, n_heads + 2 n_kv_heads, head_dim] fp16: one token's fused
+ * q|k|v projection. q_out [batch, n_heads, head_dim] = rope(q);
+ * k_cache[b, h, pos, :] = rope(k[b, h]); v_cache[b, h, pos, :] = v[b, h];
+ * caches [batch, n_kv_heads, max_len, head_dim]. cos / sin: the position's
+ * [head_dim] row of the rotary tables, as llmik_rope applies it.
+ * Replaces: rope of q and k (rope_fwd, integration/prealloc_cache.py:132-133)
+ *   and the cache-slot writes of PreallocCache.update (:61-76).
+ */
+LLMIK_API llmik_status llmik_rope_qkv_append_f16(const void* qkv, const void* cos, const void* sin,
+                                                 void* q_out, void* k_cache, void* v_cache, int batch,
+                                                 int n_heads, int n_kv_heads, int head_dim, int max_len,
+                                                 int pos, void* stream);
+
+/*
+ * h_out = fp16(x + residual) and out = llmik_rmsnorm(h_out, weight, eps),
+ * [rows, hidden] fp16, hidden % 8 == 0 and hidden <= 8192.
+ * Replaces: a decoder layer's residual add (transformers' LlamaDecoderLayer)
+ *   and the RMSNorm after it (rms_fwd, integration/prealloc_cache.py:126-127).
+ */
+LLMIK_API llmik_status llmik_add_rmsnorm(const void* x, const void* residual, const void* weight,
+                                         void* h_out, void* out, int rows, int hidden, float eps,
+                                         void* stream);
+
+/*
+ * out[r, c] = fp16(silu(gate_up[r, c]) * gate_up[r, cols + c]) over a fused
+ * gate|up projection gate_up [rows, 2 cols] fp16; cols % 8 == 0.
+ * Replaces: llmik_silu_mul on the gate and up projections' separate outputs
+ *   (mlp_fwd, integration/prealloc_cache.py:129-130).
+ */
+LLMIK_API llmik_status llmik_silu_mul_halves(const void* gate_up, void* out, long rows, int cols,
+                                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -449,7 +449,6 @@ void decode_attention_mfma_kernel(AttnParams p) {
     const int c = lane & 15;
 
     const int head0 = kvh * p.gqa + hchunk * HPW;
-    const long row_base = (long)(b * p.n_kv_heads + kvh) * p.kv_buf_len;
     const uint16_t* qrow = p.q + ((long)b * p.n_heads + head0 + (c % HPW)) * kHeadDim;
 
     // Q as the A operand (4 k-steps); for INT4 the hi/lo pair of q * k_scale.

@@ -394,4 +394,45 @@ LLMIK_API llmik_status llmik_rope(const void* x, const void* cos, const void* si
     return launch_rope(x, cos, sin, out, B, H, S, D, as_stream(stream));
 }
 
+LLMIK_API llmik_status llmik_rope_qkv_append_f16(const void* qkv, const void* cos, const void* sin,
+                                                 void* q_out, void* k_cache, void* v_cache, int batch,
+                                                 int n_heads, int n_kv_heads, int head_dim, int max_len,
+                                                 int pos, void* stream) {
+    if (batch < 0 || n_heads < 0 || n_kv_heads < 0 || head_dim < 0 || max_len < 0)
+        return invalid("negative dimension");
+    if (head_dim % 2 != 0) return invalid("head_dim must be even");
+    if (pos < 0 || pos >= max_len) return invalid("pos outside the cache");
+    if ((long)batch * (n_heads + 2L * n_kv_heads) * head_dim > 0 &&
+        (!qkv || !cos || !sin || !q_out || !k_cache || !v_cache))
+        return invalid("null pointer");
+    if ((long)batch * (n_heads + 2L * n_kv_heads) * (head_dim / 2) > 0xFFFFFFFFL * 256L)
+        return invalid("too many heads");
+    return launch_rope_qkv_append(qkv, cos, sin, q_out, k_cache, v_cache, batch, n_heads, n_kv_heads,
+                                  head_dim, max_len, pos, as_stream(stream));
+}
+
+LLMIK_API llmik_status llmik_add_rmsnorm(const void* x, const void* residual, const void* weight,
+                                         void* h_out, void* out, int rows, int hidden, float eps,
+                                         void* stream) {
+    if (rows < 0 || hidden < 0) return invalid("negative dimension");
+    if (hidden % 8 != 0 || hidden > 8192) return invalid("hidden must be a multiple of 8 and at most 8192");
+    if ((long)rows * hidden > 0 && (!x || !residual || !weight || !h_out || !out))
+        return invalid("null pointer");
+    if (!aligned(x, 16) || !aligned(residual, 16) || !aligned(weight, 16) || !aligned(h_out, 16) ||
+        !aligned(out, 16))
+        return set_error(LLMIK_ERR_ALIGNMENT, "add_rmsnorm tensors must be 16-byte aligned");
+    return launch_add_rmsnorm(x, residual, weight, h_out, out, rows, hidden, eps, as_stream(stream));
+}
+
+LLMIK_API llmik_status llmik_silu_mul_halves(const void* gate_up, void* out, long rows, int cols,
+                                             void* stream) {
+    if (rows < 0 || cols < 0) return invalid("negative dimension");
+    if (cols % 8 != 0) return invalid("cols must be a multiple of 8");
+    if (rows * cols > 0 && (!gate_up || !out)) return invalid("null pointer");
+    if ((rows * cols + 2047) / 2048 > 0xFFFFFFFFL) return invalid("too many values");
+    if (!aligned(gate_up, 16) || !aligned(out, 16))
+        return set_error(LLMIK_ERR_ALIGNMENT, "silu_mul_halves tensors must be 16-byte aligned");
+    return launch_silu_mul_halves(gate_up, out, rows, cols, as_stream(stream));
+}
+
 }  // extern "C"

@@ -110,5 +110,12 @@ int launch_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden
 int launch_silu_mul(const void* g, const void* u, void* out, long n, hipStream_t stream);
 int launch_rope(const void* x, const void* cs, const void* sn, void* out, int B, int H, int S,
                 int D, hipStream_t stream);
+// decode-step merges of the ops above
+int launch_rope_qkv_append(const void* qkv, const void* cs, const void* sn, void* q_out, void* kbuf,
+                           void* vbuf, int B, int H, int Hkv, int D, int max_len, int pos,
+                           hipStream_t stream);
+int launch_add_rmsnorm(const void* x, const void* r, const void* w, void* h_out, void* out, int rows,
+                       int hidden, float eps, hipStream_t stream);
+int launch_silu_mul_halves(const void* gu, void* out, long rows, int cols, hipStream_t stream);
 
 }  // namespace llmik

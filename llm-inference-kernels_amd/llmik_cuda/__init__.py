@@ -40,7 +40,8 @@ __all__ = [
     "decode_attention_int4", "w4a16_gemm", "w4a16_dequantize", "rmsnorm", "silu_mul", "rope",
     "w4a16_gemm_f32out", "quantize_per_token_into", "quantize_v_per_token_int4_into",
     "quantize_k_per_channel_groupwise_int4_into", "quantize_weights_int4_groupwise",
-    "pack_int4_along_k", "quantize_pack_weights_int4", "kivi_append_token_int4", "LIB_PATH",
+    "pack_int4_along_k", "quantize_pack_weights_int4", "kivi_append_token_int4", "rope_qkv_append", "add_rmsnorm", "silu_mul_halves",
+    "LIB_PATH",
 ]
 
 
@@ -605,4 +606,72 @@ def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     out = torch.empty_like(xc)
     with torch.cuda.device(x.device):
         check(lib.llmik_rope(_ptr(xc), _ptr(cc), _ptr(sc), _ptr(out), B, H, S, D, _stream(x)))
+    return out
+
+
+# ------------------------------------------------------ decode-step merges
+# One launch each for consecutive ops of the reference's patched decode step
+# (integration/prealloc_cache.py:61-76,126-133); same results as the ops they
+# replace.
+
+def rope_qkv_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                    k_cache: torch.Tensor, v_cache: torch.Tensor, pos: int) -> torch.Tensor:
+    """One token's fused q|k|v projection qkv [batch, (n_heads + 2 n_kv_heads)
+    * head_dim] fp16: returns rope(q) [batch, n_heads, head_dim] and writes
+    rope(k) and v into slot `pos` of k_cache / v_cache [batch, n_kv_heads,
+    max_len, head_dim]. cos / sin: the position's [head_dim] rotary row.
+    Equals rope(q, cos, sin), rope(k, cos, sin) and the two slot copies."""
+    _require(all(_is_device(t) for t in (qkv, cos, sin, k_cache, v_cache)), "inputs must be CUDA")
+    _require(all(t.dtype == torch.float16 for t in (qkv, cos, sin, k_cache, v_cache)), "fp16 only")
+    _require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.is_contiguous()
+             and v_cache.is_contiguous(), "caches must be contiguous [batch, n_kv_heads, max_len, head_dim]")
+    B, Hkv, max_len, D = k_cache.shape
+    _require(D % 2 == 0, "head_dim must be even")
+    _require(cos.numel() == D and sin.numel() == D, "cos/sin must be one [head_dim] row")
+    _require(qkv.size(0) == B and qkv.numel() % (B * D) == 0, "qkv must be [batch, heads * head_dim]")
+    H = qkv.numel() // (B * D) - 2 * Hkv
+    _require(H > 0, "qkv holds fewer than 2 n_kv_heads + 1 heads")
+    _require(0 <= pos < max_len, "pos outside the cache")
+    x = qkv.contiguous()
+    cc, sc = cos.contiguous(), sin.contiguous()
+    q = torch.empty((B, H, D), dtype=torch.float16, device=qkv.device)
+    with torch.cuda.device(qkv.device):
+        check(lib.llmik_rope_qkv_append_f16(_ptr(x), _ptr(cc), _ptr(sc), _ptr(q), _ptr(k_cache),
+                                            _ptr(v_cache), B, H, Hkv, D, max_len, int(pos),
+                                            _stream(qkv)))
+    return q
+
+
+def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """h = x + residual (fp16) and rmsnorm(h, weight, eps) in one launch;
+    returns (h, normed). The last dim is at most 8192, a multiple of 8."""
+    _require(all(_is_device(t) for t in (x, residual, weight)), "inputs must be CUDA")
+    _require(all(t.dtype == torch.float16 for t in (x, residual, weight)), "fp16 only")
+    _require(x.shape == residual.shape, "x and residual must have the same shape")
+    Hd = x.size(-1)
+    _require(weight.numel() == Hd, "weight length must match x last dim")
+    x2 = x.contiguous().reshape(-1, Hd)
+    r2 = residual.contiguous().reshape(-1, Hd)
+    w = weight.contiguous()
+    h = torch.empty_like(x2)
+    out = torch.empty_like(x2)
+    with torch.cuda.device(x.device):
+        check(lib.llmik_add_rmsnorm(_ptr(x2), _ptr(r2), _ptr(w), _ptr(h), _ptr(out), x2.size(0), Hd,
+                                    float(eps), _stream(x)))
+    return h.reshape(x.shape), out.reshape(x.shape)
+
+
+def silu_mul_halves(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up over a fused gate|up projection [..., 2 * cols]
+    (gate = the first half of the last dim): silu_mul of the two halves."""
+    _require(_is_device(gate_up), "inputs must be CUDA")
+    _require(gate_up.dtype == torch.float16, "fp16 only")
+    _require(gate_up.size(-1) % 16 == 0, "the last dim must be 2 * cols with cols a multiple of 8")
+    cols = gate_up.size(-1) // 2
+    gu = gate_up.contiguous()
+    rows = gu.numel() // (2 * cols) if cols else 0
+    out = torch.empty(gu.shape[:-1] + (cols,), dtype=torch.float16, device=gu.device)
+    with torch.cuda.device(gate_up.device):
+        check(lib.llmik_silu_mul_halves(_ptr(gu), _ptr(out), rows, cols, _stream(gate_up)))
     return out

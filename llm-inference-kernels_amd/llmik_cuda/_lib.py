@@ -54,6 +54,9 @@ _SIGNATURES = {
     "llmik_rmsnorm": (_i, [_p, _p, _p, _i, _i, _f, _p]),
     "llmik_silu_mul": (_i, [_p, _p, _p, _l, _p]),
     "llmik_rope": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "llmik_rope_qkv_append_f16": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
+    "llmik_add_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _p]),
+    "llmik_silu_mul_halves": (_i, [_p, _p, _l, _i, _p]),
 }
 
 for _name, (_res, _args) in _SIGNATURES.items():

@@ -13,6 +13,13 @@ projections are W4A16 `QuantizedLinear`s (integration/w4a16_patch.py:67-116).
     h = x + o_proj(decode_attention(q, kbuf, vbuf, scale, pos + 1))
     out = h + down_proj(silu_mul(gate_proj(n2), up_proj(n2))),  n2 = rmsnorm(h)
 
+With `fused=True` (the default) the step makes 10 launches instead of 17:
+q|k|v and gate|up are each one W4A16 projection over column-concatenated
+weights (codes and scales per column are those of the separate matrices),
+`rope_qkv_append` ropes q and k and writes the cache slot, `add_rmsnorm`
+takes the residual add and the second norm, and `silu_mul_halves` reads the
+fused gate|up output. `fused=False` runs the op-by-op sequence above.
+
 Every op enqueues on the current stream without a host synchronisation, the
 split-K reductions are deterministic and the per-stream workspace is reused,
 so `capture(x, pos)` records one step in a `torch.cuda.CUDAGraph` whose
@@ -27,7 +34,8 @@ from typing import Dict, Optional, Tuple
 
 import torch
 
-from . import decode_attention, quantize_pack_weights_int4, rmsnorm, rope, silu_mul, w4a16_gemm
+from . import (add_rmsnorm, decode_attention, quantize_pack_weights_int4, rmsnorm, rope,
+               rope_qkv_append, silu_mul, silu_mul_halves, w4a16_gemm)
 
 
 class W4Linear:
@@ -61,14 +69,17 @@ class DecodeLayer:
     `weights` maps q, k, v, o, gate, up, down to [in, out] fp32 matrices and
     ln1, ln2 to [hidden] fp16 vectors; missing entries are drawn from a seeded
     generator (N(0, 0.02) matrices, N(1, 0.1) norm weights). Only the packed
-    codes and fp16 scales of the matrices are kept."""
+    codes and fp16 scales of the matrices are kept: in `proj` under their
+    names, or with `fused=True` as "qkv" and "gate_up" column concatenations;
+    `columns[name]` gives (key in `proj`, first column, end column)."""
 
     NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
     def __init__(self, hidden: int, n_heads: int, n_kv_heads: int, intermediate: int, batch: int,
                  max_len: int, device: Optional[torch.device] = None, head_dim: int = 128,
                  group_size: int = 128, eps: float = 1e-5, rope_theta: float = 500000.0,
-                 weights: Optional[Dict[str, torch.Tensor]] = None, seed: int = 0) -> None:
+                 weights: Optional[Dict[str, torch.Tensor]] = None, seed: int = 0,
+                 fused: bool = True) -> None:
         if n_heads * head_dim != hidden or n_heads % n_kv_heads != 0:
             raise RuntimeError("hidden must be n_heads * head_dim and n_heads a multiple of n_kv_heads")
         dev = torch.device("cuda") if device is None else torch.device(device)
@@ -87,15 +98,29 @@ class DecodeLayer:
         for name in ("ln1", "ln2"):
             if name not in weights:
                 weights[name] = (1.0 + 0.1 * torch.randn(hidden, generator=gen, device=dev)).half()
-        self.proj = {name: W4Linear(weights.pop(name), group_size) for name in self.NAMES}
+        # the merged kernels' limits: add_rmsnorm rows of at most 8192, 16-byte vectors
+        self.fused = fused and hidden % 8 == 0 and hidden <= 8192 and intermediate % 8 == 0
+        if self.fused:
+            cat = lambda *ns: torch.cat([weights.pop(n) for n in ns], dim=1)  # noqa: E731
+            self.proj = {"qkv": W4Linear(cat("q", "k", "v"), group_size), "o": W4Linear(weights.pop("o"), group_size),
+                         "gate_up": W4Linear(cat("gate", "up"), group_size),
+                         "down": W4Linear(weights.pop("down"), group_size)}
+            self.columns = {"q": ("qkv", 0, hidden), "k": ("qkv", hidden, hidden + kv),
+                            "v": ("qkv", hidden + kv, hidden + 2 * kv), "o": ("o", 0, hidden),
+                            "gate": ("gate_up", 0, intermediate),
+                            "up": ("gate_up", intermediate, 2 * intermediate), "down": ("down", 0, hidden)}
+        else:
+            self.proj = {name: W4Linear(weights.pop(name), group_size) for name in self.NAMES}
+            self.columns = {name: (name, 0, shapes[name][1]) for name in self.NAMES}
         self.ln1 = weights["ln1"].to(dev, torch.float16).contiguous()
         self.ln2 = weights["ln2"].to(dev, torch.float16).contiguous()
         self.cos, self.sin = rope_tables(max_len, head_dim, rope_theta, dev)
-        # Per-position tables already broadcast over the batch ([max_len,
-        # batch, D]): rope takes a position's [batch, 1, D] slice as is,
-        # where a [1, D] slice would be expanded by a copy on every call.
-        self.cos_b = self.cos[:, None, :].expand(max_len, batch, head_dim).contiguous()
-        self.sin_b = self.sin[:, None, :].expand(max_len, batch, head_dim).contiguous()
+        if not self.fused:
+            # Per-position tables already broadcast over the batch ([max_len,
+            # batch, D]): rope takes a position's [batch, 1, D] slice as is,
+            # where a [1, D] slice would be expanded by a copy on every call.
+            self.cos_b = self.cos[:, None, :].expand(max_len, batch, head_dim).contiguous()
+            self.sin_b = self.sin[:, None, :].expand(max_len, batch, head_dim).contiguous()
         shape = (batch, n_kv_heads, max_len, head_dim)
         self.kbuf = torch.zeros(shape, dtype=torch.float16, device=dev)
         self.vbuf = torch.zeros(shape, dtype=torch.float16, device=dev)
@@ -110,6 +135,11 @@ class DecodeLayer:
         B, H, Hkv, D = self.batch, self.n_heads, self.n_kv_heads, self.head_dim
         p = self.proj
         n1 = rmsnorm(x, self.ln1, self.eps)
+        if self.fused:
+            q = rope_qkv_append(p["qkv"](n1), self.cos[pos], self.sin[pos], self.kbuf, self.vbuf, pos)
+            attn = decode_attention(q, self.kbuf, self.vbuf, self.scale, pos + 1)
+            h, n2 = add_rmsnorm(x, p["o"](attn.view(B, H * D)), self.ln2, self.eps)
+            return h + p["down"](silu_mul_halves(p["gate_up"](n2)))
         cos, sin = self.cos_b[pos].view(B, 1, D), self.sin_b[pos].view(B, 1, D)
         q = rope(p["q"](n1).view(B, H, 1, D), cos, sin)
         k = rope(p["k"](n1).view(B, Hkv, 1, D), cos, sin)

@@ -110,6 +110,16 @@ def test_c_layer_argument_errors(lib):
     assert st == -1 and "1..128" in _err(lib)
     st = lib.llmik_kivi_append_token_int4(*kivi, 64, 64, 32, 0, S)
     assert st == -1 and "head_dim=128" in _err(lib)
+    st = lib.llmik_rope_qkv_append_f16(16, 16, 16, 16, 16, 16, 2, 4, 2, 128, 8, 8, S)
+    assert st == -1 and "pos outside" in _err(lib)
+    st = lib.llmik_rope_qkv_append_f16(16, 16, 16, 16, 16, 16, 2, 4, 2, 9, 8, 0, S)
+    assert st == -1 and "even" in _err(lib)
+    st = lib.llmik_add_rmsnorm(16, 16, 16, 16, 16, 2, 8200, 1e-5, S)
+    assert st == -1 and "at most 8192" in _err(lib)
+    st = lib.llmik_add_rmsnorm(16, 16, 16, 16, 18, 2, 4096, 1e-5, S)
+    assert st == -4
+    st = lib.llmik_silu_mul_halves(16, 16, 2, 12, S)
+    assert st == -1 and "multiple of 8" in _err(lib)
 
 
 def test_workspace_sizes_without_gpu(lib):

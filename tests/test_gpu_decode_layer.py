@@ -7,6 +7,9 @@ eager and captured in a HIP graph.
   sequence restated on the CPU from the oracle's pieces (oracle/fused.py,
   oracle/attention.py, oracle/w4a16.py), rounding to fp16 where the GPU ops
   hand fp16 tensors to each other.
+* Both forms of the step are checked: the merged one (q|k|v and gate|up
+  projections, rope + cache write, residual add + RMSNorm in one launch
+  each) and the op-by-op one.
 * Graph replays reproduce the eager step bit for bit: every llmik kernel is
   deterministic (fixed-order split-K reductions), and the module's
   per-stream workspace keeps its counters zero between calls. Replays are
@@ -28,9 +31,9 @@ CFG = dict(hidden=512, n_heads=4, n_kv_heads=2, intermediate=1024, batch=4, max_
 POS = 129
 
 
-def _layer(cuda, seed=0):
+def _layer(cuda, seed=0, fused=True):
     from llmik_cuda.decode_layer import DecodeLayer
-    layer = DecodeLayer(device=cuda, seed=seed, **CFG)
+    layer = DecodeLayer(device=cuda, seed=seed, fused=fused, **CFG)
     g = torch.Generator(device=cuda).manual_seed(seed + 100)
     # context already in the cache for positions < POS
     layer.kbuf[:, :, :POS] = torch.randn(layer.kbuf[:, :, :POS].shape, generator=g, device=cuda).half()
@@ -43,9 +46,12 @@ def _x(cuda, seed):
     return torch.randn((CFG["batch"], CFG["hidden"]), generator=g, device=cuda).half()
 
 
-def _w_hat(lin) -> np.ndarray:
+def _w_hat(layer, name) -> np.ndarray:
+    key, a, b = layer.columns[name]
+    lin = layer.proj[key]
     codes = ow.unpack_int4_along_k(lin.weight_packed.cpu().numpy())
-    return ow.dequantize_weights_int4_groupwise(codes, lin.scale.cpu().numpy(), lin.group_size)
+    w = ow.dequantize_weights_int4_groupwise(codes, lin.scale.cpu().numpy(), lin.group_size)
+    return w[:, a:b]
 
 
 def _h(a: np.ndarray) -> np.ndarray:
@@ -54,7 +60,7 @@ def _h(a: np.ndarray) -> np.ndarray:
 
 def _oracle_step(layer, x16: np.ndarray, kbuf: np.ndarray, vbuf: np.ndarray, pos: int) -> np.ndarray:
     B, H, Hkv, D = layer.batch, layer.n_heads, layer.n_kv_heads, layer.head_dim
-    W = {n: _w_hat(layer.proj[n]) for n in layer.NAMES}
+    W = {n: _w_hat(layer, n) for n in layer.NAMES}
     mm = lambda a, n: _h(a.astype(np.float32) @ W[n])   # noqa: E731  fp32 accumulate, fp16 out
     cos = np.broadcast_to(layer.cos[pos:pos + 1].cpu().numpy()[None], (B, 1, D))
     sin = np.broadcast_to(layer.sin[pos:pos + 1].cpu().numpy()[None], (B, 1, D))
@@ -72,8 +78,10 @@ def _oracle_step(layer, x16: np.ndarray, kbuf: np.ndarray, vbuf: np.ndarray, pos
     return _h(h.astype(np.float32) + mm(m, "down").astype(np.float32))
 
 
-def test_decode_step_matches_oracle_composition(llmik, cuda):
-    layer = _layer(cuda)
+@pytest.mark.parametrize("fused", [True, False])
+def test_decode_step_matches_oracle_composition(llmik, cuda, fused):
+    layer = _layer(cuda, fused=fused)
+    assert layer.fused == fused
     x = _x(cuda, 1)
     k0, v0 = layer.kbuf.cpu().numpy(), layer.vbuf.cpu().numpy()
     got = layer.step(x, POS).cpu().numpy().astype(np.float32)
@@ -88,8 +96,9 @@ def test_decode_step_matches_oracle_composition(llmik, cuda):
     assert not torch.equal(layer.kbuf[:, :, POS].cpu(), torch.from_numpy(k0[:, :, POS]))
 
 
-def test_graph_replays_reproduce_eager_step(llmik, cuda):
-    layer = _layer(cuda, seed=3)
+@pytest.mark.parametrize("fused", [True, False])
+def test_graph_replays_reproduce_eager_step(llmik, cuda, fused):
+    layer = _layer(cuda, seed=3, fused=fused)
     x = _x(cuda, 4)
     eager = layer.step(x, POS).clone()
     graph, out = layer.capture(x, POS)

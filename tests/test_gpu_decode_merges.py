@@ -1,0 +1,85 @@
+"""GPU: the decode-step merges (rope_qkv_append, add_rmsnorm,
+silu_mul_halves) give the same bits as the ops they replace, which the fused
+op tests pin against the fp32 oracle; add_rmsnorm is also checked against the
+oracle directly."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fused as of
+from tests.helpers import randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,max_len,pos", [
+    (8, 32, 8, 128, 64, 17),     # Llama-3-8B heads
+    (4, 4, 2, 128, 160, 159),    # last slot
+    (3, 6, 3, 64, 5, 0),         # first slot, head_dim 64
+    (1, 2, 1, 10, 3, 1),         # head_dim not a multiple of 8
+])
+def test_rope_qkv_append_equals_rope_and_slot_copies(llmik, cuda, B, H, Hkv, D, max_len, pos):
+    qkv = _dev(randn((B, (H + 2 * Hkv) * D), 1).astype(np.float16), cuda)
+    cos = _dev(randn((D,), 2).astype(np.float16), cuda)
+    sin = _dev(randn((D,), 3).astype(np.float16), cuda)
+    kc = _dev(randn((B, Hkv, max_len, D), 4).astype(np.float16), cuda)
+    vc = _dev(randn((B, Hkv, max_len, D), 5).astype(np.float16), cuda)
+    k_ref, v_ref = kc.clone(), vc.clone()
+    parts = qkv.view(B, H + 2 * Hkv, D)
+    cs = cos.view(1, 1, D).expand(B, 1, D)
+    sn = sin.view(1, 1, D).expand(B, 1, D)
+    q_ref = llmik.rope(parts[:, :H].contiguous().view(B, H, 1, D), cs, sn).view(B, H, D)
+    k_ref[:, :, pos] = llmik.rope(parts[:, H:H + Hkv].contiguous().view(B, Hkv, 1, D), cs, sn)[:, :, 0]
+    v_ref[:, :, pos] = parts[:, H + Hkv:]
+    q = llmik.rope_qkv_append(qkv, cos, sin, kc, vc, pos)
+    assert q.shape == (B, H, D)
+    assert torch.equal(q, q_ref)
+    assert torch.equal(kc, k_ref)      # slot pos rewritten, every other slot untouched
+    assert torch.equal(vc, v_ref)
+
+
+@pytest.mark.parametrize("rows,hidden", [(8, 4096), (1, 8192), (3, 520), (5, 2056), (2, 6144)])
+def test_add_rmsnorm_equals_add_then_rmsnorm(llmik, cuda, rows, hidden):
+    x16 = randn((rows, hidden), 6).astype(np.float16)
+    r16 = randn((rows, hidden), 7).astype(np.float16)
+    w16 = randn((hidden,), 8).astype(np.float16)
+    x, r, w = _dev(x16, cuda), _dev(r16, cuda), _dev(w16, cuda)
+    h, n = llmik.add_rmsnorm(x, r, w, 1e-5)
+    h_ref = x + r
+    assert torch.equal(h, h_ref)
+    assert torch.equal(n, llmik.rmsnorm(h_ref, w, 1e-5))
+    # and against the oracle: h is the one fp16 rounding of the fp32 sum
+    h_np = (x16.astype(np.float32) + r16.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(h.cpu().numpy(), h_np)
+    ref = of.rmsnorm(h_np, w16, 1e-5)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+    assert (np.abs(n.float().cpu().numpy() - ref) <= ulp + 1e-5 * np.abs(ref) + 1e-7).all()
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 14336), (1, 1024), (3, 8), (16, 520)])
+def test_silu_mul_halves_equals_silu_mul(llmik, cuda, rows, cols):
+    gu = _dev(randn((rows, 2 * cols), 9).astype(np.float16), cuda)
+    out = llmik.silu_mul_halves(gu)
+    assert out.shape == (rows, cols)
+    assert torch.equal(out, llmik.silu_mul(gu[:, :cols].contiguous(), gu[:, cols:].contiguous()))
+
+
+def test_merges_reject_bad_shapes(llmik, cuda):
+    kc = torch.zeros((2, 2, 4, 128), dtype=torch.float16, device=cuda)
+    cs = torch.zeros(128, dtype=torch.float16, device=cuda)
+    qkv = torch.zeros((2, 6 * 128), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="pos outside the cache"):
+        llmik.rope_qkv_append(qkv, cs, cs, kc, kc.clone(), 4)
+    with pytest.raises(RuntimeError, match="fewer than"):
+        llmik.rope_qkv_append(qkv[:, :4 * 128], cs, cs, kc, kc.clone(), 0)
+    x = torch.zeros((2, 8200), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="at most 8192"):
+        llmik.add_rmsnorm(x, x, x[0], 1e-5)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        llmik.silu_mul_halves(torch.zeros((2, 24), dtype=torch.float16, device=cuda))
