@@ -1707,6 +1707,13 @@ static int stream_override() {
     return (*e == '0') ? 0 : 1;
 }
 
+// LLMIK_W4A16_STREAM_SPLITS=n forces the streaming GEMV's K split count
+// (clamped to what the K extent allows), for measurement.
+static int stream_splits_override() {
+    const char* e = getenv("LLMIK_W4A16_STREAM_SPLITS");
+    return (e == nullptr || *e == '\0') ? -1 : atoi(e);
+}
+
 GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     GemmPlan pl{};
     const bool pow2_group = group_size >= 32 && (group_size & (group_size - 1)) == 0;
@@ -1722,6 +1729,8 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
         const int tiles = N / 64;
         long want = (long)device_cu_count() / tiles;
         if (want < 1 || tiles > kMaxCounters) want = 1;
+        const int forced = stream_splits_override();
+        if (forced > 0 && tiles <= kMaxCounters) want = forced;
         if (want > steps / 2) want = steps / 2 > 0 ? steps / 2 : 1;
         const int need = (int)((steps + want - 1) / want);
         int best_nw = kStreamMaxWaves, best_ws = 0;
