@@ -315,3 +315,41 @@ def test_token_row_stride_of_slices(mod):
     assert mod._token_rows(buf[:, :1, 3:9]) == 120   # rows of one head: batch stride
     with pytest.raises(RuntimeError):
         mod._token_rows(buf[:, ::2])   # unequally spaced rows (3 heads, stride 2)
+
+
+# ------------------------------------------- decode-step merges and KIVI append
+
+@pytest.mark.parametrize("case", [
+    (lambda m: m.rope_qkv_append(_t(2, 6 * 128), _t(128), _t(128), _t(2, 2, 4, 128), _t(2, 2, 4, 128), 4),
+     "pos outside the cache"),
+    (lambda m: m.rope_qkv_append(_t(2, 4 * 128), _t(128), _t(128), _t(2, 2, 4, 128), _t(2, 2, 4, 128), 0),
+     "fewer than 2 n_kv_heads"),
+    (lambda m: m.rope_qkv_append(_t(2, 6 * 128), _t(64), _t(64), _t(2, 2, 4, 128), _t(2, 2, 4, 128), 0),
+     "one \\[head_dim\\] row"),
+    (lambda m: m.rope_qkv_append(_t(2, 6 * 128), _t(128), _t(128), _t(2, 2, 4, 128),
+                                 _t(2, 2, 4, 128, dtype=torch.float32), 0), "fp16 only"),
+    (lambda m: m.add_rmsnorm(_t(2, 64), _t(2, 32), _t(64), 1e-5), "same shape"),
+    (lambda m: m.add_rmsnorm(_t(2, 64), _t(2, 64), _t(32), 1e-5), "weight length"),
+    (lambda m: m.silu_mul_halves(_t(2, 24)), "multiple of 8"),
+    (lambda m: m.kivi_append_token_int4(_t(1, 8, 1, 128), _t(1, 8, 1, 128), _t(1, 8, 16, 128),
+                                        _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 2, 128),
+                                        _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 64), 5, 32),
+     "k_open must be"),
+    (lambda m: m.kivi_append_token_int4(_t(1, 8, 1, 128), _t(1, 8, 1, 128), _t(1, 8, 32, 128),
+                                        _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 2, 128, dtype=torch.float32),
+                                        _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 64), 5, 32),
+     "must be fp16"),
+])
+def test_python_merge_and_append_validation(as_device, case):
+    fn, msg = case
+    with pytest.raises(RuntimeError, match=msg):
+        fn(as_device)
+
+
+def test_merges_check_device_first(mod):
+    with pytest.raises(RuntimeError, match="inputs must be CUDA"):
+        mod.add_rmsnorm(_t(2, 64), _t(2, 64), _t(64), 1e-5)
+    with pytest.raises(RuntimeError, match="all inputs must be CUDA tensors"):
+        mod.kivi_append_token_int4(_t(1, 8, 1, 128), _t(1, 8, 1, 128), _t(1, 8, 32, 128),
+                                   _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 2, 128),
+                                   _t(1, 8, 64, 64, dtype=torch.int8), _t(1, 8, 64), 5, 32)
