@@ -269,10 +269,11 @@ def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmu
     rmsnorm, W4A16 q/k/v/o/gate/up/down, rope, fp16 cache write, split-K
     attention over `ctx` tokens, silu_mul, residual adds), launched eagerly
     from Python and replayed from one HIP graph; `fused` picks the merged
-    10-launch step or the op-by-op 17-launch one. Four layers hold ~950 MB of
-    weights and caches, so the replays read HBM, not the Infinity Cache."""
+    step (a DecodeStack: 9 launches per layer plus one) or the op-by-op
+    17-launch one. Four layers hold ~950 MB of weights and caches, so the
+    replays read HBM, not the Infinity Cache."""
     import torch
-    from llmik_cuda.decode_layer import DecodeLayer
+    from llmik_cuda.decode_layer import DecodeLayer, DecodeStack
     dev = torch.device("cuda:0")
     layers = []
     for i in range(n_layers):
@@ -285,10 +286,18 @@ def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmu
     x = torch.randn((B, 4096), generator=torch.Generator(device=dev).manual_seed(60), device=dev,
                     dtype=torch.float16)
 
-    def model_step(inp):
-        for layer in layers:
-            inp = layer.step(inp, pos)
-        return inp
+    if fused:
+        # the merged layers hand (h, mlp) on; the residual add rides in the
+        # next layer's first RMSNorm launch
+        stack = DecodeStack(layers)
+
+        def model_step(inp):
+            return stack.step(inp, pos)
+    else:
+        def model_step(inp):
+            for layer in layers:
+                inp = layer.step(inp, pos)
+            return inp
 
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):

@@ -19,6 +19,8 @@ weights (codes and scales per column are those of the separate matrices),
 `rope_qkv_append` ropes q and k and writes the cache slot, `add_rmsnorm`
 takes the residual add and the second norm, and `silu_mul_halves` reads the
 fused gate|up output. `fused=False` runs the op-by-op sequence above.
+`DecodeStack` runs merged layers in sequence with each layer's last residual
+add carried into the next layer's first RMSNorm launch.
 
 Every op enqueues on the current stream without a host synchronisation, the
 split-K reductions are deterministic and the per-stream workspace is reused,
@@ -132,14 +134,12 @@ class DecodeLayer:
         0..pos."""
         if not 0 <= pos < self.max_len:
             raise RuntimeError(f"position {pos} outside the cache (max_len {self.max_len})")
+        if self.fused:
+            h, mlp = self.step_parts(x, pos)
+            return h + mlp
         B, H, Hkv, D = self.batch, self.n_heads, self.n_kv_heads, self.head_dim
         p = self.proj
         n1 = rmsnorm(x, self.ln1, self.eps)
-        if self.fused:
-            q = rope_qkv_append(p["qkv"](n1), self.cos[pos], self.sin[pos], self.kbuf, self.vbuf, pos)
-            attn = decode_attention(q, self.kbuf, self.vbuf, self.scale, pos + 1)
-            h, n2 = add_rmsnorm(x, p["o"](attn.view(B, H * D)), self.ln2, self.eps)
-            return h + p["down"](silu_mul_halves(p["gate_up"](n2)))
         cos, sin = self.cos_b[pos].view(B, 1, D), self.sin_b[pos].view(B, 1, D)
         q = rope(p["q"](n1).view(B, H, 1, D), cos, sin)
         k = rope(p["k"](n1).view(B, Hkv, 1, D), cos, sin)
@@ -150,18 +150,66 @@ class DecodeLayer:
         n2 = rmsnorm(h, self.ln2, self.eps)
         return h + p["down"](silu_mul(p["gate"](n2), p["up"](n2)))
 
+    def step_parts(self, x: torch.Tensor, pos: int,
+                   residual: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        """The merged step without its last residual add: returns (h, mlp)
+        with step(x, pos) == h + mlp. With `residual`, the layer's input is
+        x + residual, added by the first RMSNorm's launch (add_rmsnorm), so
+        a stack of layers hands (h, mlp) on without a separate add."""
+        if not self.fused:
+            raise RuntimeError("step_parts needs a layer built with fused=True")
+        if not 0 <= pos < self.max_len:
+            raise RuntimeError(f"position {pos} outside the cache (max_len {self.max_len})")
+        B, H, D = self.batch, self.n_heads, self.head_dim
+        p = self.proj
+        if residual is None:
+            n1 = rmsnorm(x, self.ln1, self.eps)
+        else:
+            x, n1 = add_rmsnorm(x, residual, self.ln1, self.eps)
+        q = rope_qkv_append(p["qkv"](n1), self.cos[pos], self.sin[pos], self.kbuf, self.vbuf, pos)
+        attn = decode_attention(q, self.kbuf, self.vbuf, self.scale, pos + 1)
+        h, n2 = add_rmsnorm(x, p["o"](attn.view(B, H * D)), self.ln2, self.eps)
+        return h, p["down"](silu_mul_halves(p["gate_up"](n2)))
+
     def capture(self, x: torch.Tensor, pos: int, warmup: int = 2) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
         """Record `step(x, pos)` in a CUDA (HIP) graph. Returns the graph and
         its output tensor; `graph.replay()` reruns the step on whatever `x`
         holds then. The warm-up steps on the capture stream set up the
         module's per-stream workspace before capture."""
-        stream = torch.cuda.Stream(device=x.device)
-        stream.wait_stream(torch.cuda.current_stream(x.device))
-        with torch.cuda.stream(stream):
-            for _ in range(warmup):
-                self.step(x, pos)
-        stream.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            out = self.step(x, pos)
-        return graph, out
+        return _capture(self.step, x, pos, warmup)
+
+
+class DecodeStack:
+    """Merged-step layers run in sequence for one token. Layer i's last
+    residual add goes into layer i + 1's first RMSNorm launch
+    (`step_parts(..., residual=)`), so n layers make 9 n + 1 launches; the
+    output equals chaining `layer.step` bit for bit (the merged norm rounds
+    x + residual exactly as the add it replaces)."""
+
+    def __init__(self, layers) -> None:
+        self.layers = list(layers)
+        if not self.layers or not all(layer.fused for layer in self.layers):
+            raise RuntimeError("DecodeStack needs one or more layers built with fused=True")
+
+    def step(self, x: torch.Tensor, pos: int) -> torch.Tensor:
+        h, r = x, None
+        for layer in self.layers:
+            h, r = layer.step_parts(h, pos, r)
+        return h + r
+
+    def capture(self, x: torch.Tensor, pos: int, warmup: int = 2) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
+        """As DecodeLayer.capture, for the whole stack."""
+        return _capture(self.step, x, pos, warmup)
+
+
+def _capture(step, x: torch.Tensor, pos: int, warmup: int) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
+    stream = torch.cuda.Stream(device=x.device)
+    stream.wait_stream(torch.cuda.current_stream(x.device))
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step(x, pos)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = step(x, pos)
+    return graph, out

@@ -122,3 +122,23 @@ def test_position_bounds(llmik, cuda):
     layer = _layer(cuda)
     with pytest.raises(RuntimeError, match="outside the cache"):
         layer.step(_x(cuda, 1), CFG["max_len"])
+
+
+def test_stack_equals_chained_layer_steps(llmik, cuda):
+    """DecodeStack hands (h, mlp) from layer to layer and adds them in the
+    next layer's first RMSNorm launch: the same bits as chaining step()."""
+    from llmik_cuda.decode_layer import DecodeStack
+    layers = [_layer(cuda, seed=s) for s in (5, 6, 7)]
+    x = _x(cuda, 8)
+    chained = x
+    for layer in layers:
+        chained = layer.step(chained, POS)
+    stack = DecodeStack(layers)
+    assert torch.equal(stack.step(x, POS), chained)
+    graph, out = stack.capture(x, POS)
+    for r in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, chained), f"replay {r}"
+    with pytest.raises(RuntimeError, match="fused=True"):
+        DecodeStack([_layer(cuda, seed=9, fused=False)])
