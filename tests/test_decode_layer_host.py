@@ -30,3 +30,17 @@ def test_layer_shape_validation():
     with pytest.raises(RuntimeError, match="multiple of n_kv_heads"):
         DecodeLayer(hidden=384, n_heads=3, n_kv_heads=2, intermediate=1024, batch=1, max_len=8,
                     device="cpu")
+
+
+def test_stack_needs_merged_layers():
+    from llmik_cuda.decode_layer import DecodeStack
+
+    class _Layer:
+        def __init__(self, fused):
+            self.fused = fused
+
+    with pytest.raises(RuntimeError, match="fused=True"):
+        DecodeStack([])
+    with pytest.raises(RuntimeError, match="fused=True"):
+        DecodeStack([_Layer(True), _Layer(False)])
+    assert len(DecodeStack([_Layer(True), _Layer(True)]).layers) == 2
