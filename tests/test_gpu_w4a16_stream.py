@@ -6,7 +6,8 @@ The shapes are chosen so that the planner's choices are all exercised:
 two-stage LDS reduction with and without a partner wave); one split and
 several, with a short last split and waves past the end of the K range;
 scale groups of 32..512 (a flush per group, or per batch inside a longer
-group); M = 1 and 2..16.
+group); M = 1 and 2..16; more tiles than CUs (a second round of
+workgroups); and split counts forced with LLMIK_W4A16_STREAM_SPLITS.
 
 The library serves these shapes with the streaming kernel when the packed
 weights reach 16 MiB; the tests set LLMIK_W4A16_STREAM=1 so that the small
@@ -44,6 +45,9 @@ CASES = [
     (7, 2048, 8192, 128),      # 2 splits, 7 rows
     (1, 32, 64, 32),           # one step: 8 waves, 7 of them idle
     (16, 96, 128, 32),         # three steps, 16 rows
+    (8, 4096, 28672, 128),     # 448 tiles, more than the CUs: no split, a second round
+                               # of workgroups (a decode step's fused gate|up)
+    (8, 4096, 6144, 128),      # 96 tiles, 2 splits (a decode step's fused q|k|v)
 ]
 
 
@@ -83,6 +87,15 @@ def test_stream_gemv(llmik, cuda, M, K, N, gs):
     err = (out32.double() - ref).abs().max().item()
     assert err <= TOL, f"max-abs {err:.3e}"
     assert torch.equal(out16.view(torch.int16), out32.half().view(torch.int16))
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 5, 8])
+def test_stream_forced_splits(llmik, cuda, monkeypatch, splits):
+    """LLMIK_W4A16_STREAM_SPLITS forces the K split count; every count gives
+    results within the gate, and the same fp16 bits as its own fp32 call."""
+    monkeypatch.setenv("LLMIK_W4A16_STREAM_SPLITS", str(splits))
+    test_stream_gemv(llmik, cuda, 8, 4096, 6144, 128)
+    test_stream_gemv(llmik, cuda, 1, 4096, 28672, 128)
 
 
 def test_stream_repeated_calls_bitwise(llmik, cuda):
