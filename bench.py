@@ -13,18 +13,21 @@ in-place quantised KV appends and the GPU weight quantiser.
 Method
   * Inputs are generated on the GPU from a seeded generator and are resident
     in HBM before timing. Each config rotates over enough distinct input
-    sets (>= 768 MB in total) that every step reads from HBM rather than the
-    256 MB Infinity Cache.
+    sets (>= 768 MiB in total, three times the 256 MB Infinity Cache) that
+    every step reads from HBM; a detail row's graph holds at least one call
+    per set, so every set is read once per replay.
   * The K timed steps are captured in one HIP graph on a dedicated stream and
     replayed once; HIP events recorded on that stream bracket the replay,
     with torch.cuda.synchronize() on both sides. Per-launch time = elapsed/K.
-  * Before timing, every config is checked against an fp32 torch computation
-    on the GPU (max-abs 2e-3); a failing config aborts the run.
+  * Before timing, every config is checked against a float64 torch
+    computation on the GPU (max-abs 2e-3); a failing config aborts the run.
   * roofline.achieved = algorithmic bytes per launch / per-launch time, with
     the byte counts stated in DESIGN.md; peak = 8 TB/s (MI355X HBM3E).
-  * cpu_baseline: the oracle's eager fp32 attention (the reference's
-    repeat_interleave form, oracle/attention.py) on the host cores, timed on
-    a bounded sample of the same workload.
+  * cpu_baseline: the reference's eager fp32 attention restated with torch
+    CPU ops (oracle/torch_ref.py: repeat_interleave GQA, fp32 matmul,
+    softmax, matmul, .to(fp16)) on the host cores given by
+    os.sched_getaffinity (capped by OMP_NUM_THREADS), median of >= 10 calls
+    after 3 warm-up calls, at the headline shape.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-details] [--no-cpu]
 """
@@ -72,11 +75,14 @@ def w4a16_bytes(M: int, K: int, N: int, gs: int = 128) -> int:
 
 # ----------------------------------------------------------------- timing
 
-def time_steps(steps_fns, warmup: int, reps: int):
+def time_steps(steps_fns, warmup: int, reps: int, all_sets: bool = True):
     """Warm up eagerly, capture `reps` steps (cycling through steps_fns) in a
     HIP graph and time one replay with events on the capture stream.
-    Returns per-step microseconds."""
+    With `all_sets`, the graph holds at least one step per input set, so a
+    replay reads every set. Returns per-step microseconds."""
     import torch
+    if all_sets:
+        reps = max(reps, len(steps_fns))
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         for i in range(max(warmup, len(steps_fns))):
@@ -101,34 +107,45 @@ def time_steps(steps_fns, warmup: int, reps: int):
 
 
 def n_sets_for(bytes_per_set: int) -> int:
-    return max(2, min(16, math.ceil(ROTATE_BYTES / max(1, bytes_per_set))))
+    """Input sets whose total is >= ROTATE_BYTES (at most 512)."""
+    return max(2, min(512, math.ceil(ROTATE_BYTES / max(1, bytes_per_set))))
 
 
 # ------------------------------------------------------------ correctness gates
 
 def torch_attention_ref(q, k, v, scale):
-    """fp32 GQA attention on the GPU (grouped, no KV expansion)."""
+    """float64 GQA attention on the GPU (grouped, no KV expansion)."""
     import torch
     B, H, D = q.shape
     Hkv = k.shape[1]
     G = H // Hkv
-    qf = q.float().reshape(B, Hkv, G, D)
-    s = torch.matmul(qf, k.float().transpose(-1, -2).contiguous()) * scale
+    qf = q.double().reshape(B, Hkv, G, D)
+    s = torch.matmul(qf, k.double().transpose(-1, -2).contiguous()) * scale
     p = torch.softmax(s, dim=-1)
-    return torch.matmul(p, v.float()).reshape(B, H, D)
+    return torch.matmul(p, v.double()).reshape(B, H, D)
 
 
 def gate(name: str, got, ref) -> float:
-    err = float((got.float() - ref.float()).abs().max())
+    err = float((got.double() - ref.double()).abs().max())
     if not err <= GATE_TOL:
         raise SystemExit(f"correctness gate failed for {name}: max-abs {err:.3e} > {GATE_TOL}")
     return err
 
 
+def excess_over_output_rounding(got, ref) -> float:
+    """max(|got - ref| - half an fp16 ulp of ref): the error that is not the
+    fp16 output's own rounding."""
+    import torch
+    a = ref.abs().to(torch.float16)
+    nxt = torch.nextafter(a, torch.full_like(a, float("inf"))).double()
+    half_ulp = (nxt - a.double()) / 2
+    return float(((got.double() - ref.double()).abs() - half_ulp).max())
+
+
 # ------------------------------------------------------------------ configs
 
 def bench_attention(llmik, fmt: str, B: int, S: int, steps: int, warmup: int, gs: int = 128,
-                    H: int = 32, Hkv: int = 8, seed: int = 0):
+                    H: int = 32, Hkv: int = 8, seed: int = 0, exact_steps: bool = False):
     import torch
     dev = torch.device("cuda:0")
     D = 128
@@ -167,9 +184,10 @@ def bench_attention(llmik, fmt: str, B: int, S: int, steps: int, warmup: int, gs
         got = llmik.decode_attention_int4(q0, kq, ks, vq, vs, gs, scale)
         kd = unpack_int4(kq[:gb]).float() * ks[:gb].float().repeat_interleave(gs, dim=2)[:, :, :S]
         vd = unpack_int4(vq[:gb]).float() * vs[:gb].float()[..., None]
-    err = gate(f"{fmt} attention B={B} S={S}", got[:gb],
-               torch_attention_ref(q0[:gb], kd, vd, scale))
-    del kd, vd, got
+    ref = torch_attention_ref(q0[:gb], kd, vd, scale)
+    err = gate(f"{fmt} attention B={B} S={S}", got[:gb], ref)
+    excess = excess_over_output_rounding(got[:gb], ref)
+    del kd, vd, got, ref
 
     if fmt == "fp16":
         fns = [lambda s=s: llmik.decode_attention(s[0], s[1], s[2], scale) for s in sets]
@@ -179,13 +197,15 @@ def bench_attention(llmik, fmt: str, B: int, S: int, steps: int, warmup: int, gs
     else:
         fns = [lambda s=s: llmik.decode_attention_int4(s[0], s[1], s[2], s[3], s[4], gs, scale)
                for s in sets]
-    us = time_steps(fns, warmup, steps)
+    us = time_steps(fns, warmup, steps, all_sets=not exact_steps)
     del sets, fns
     torch.cuda.empty_cache()
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"name": f"attn_{fmt}" + (f"_g{gs}" if fmt == "int4" else ""), "B": B, "S": S,
             "us": round(us, 3), "bytes": nbytes, "GBps": round(gbs, 1),
-            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "max_abs_err": err, "sets": n_sets}
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "max_abs_err": err,
+            "max_err_minus_out_half_ulp": excess, "sets": n_sets,
+            "rotated_MB": round(n_sets * nbytes / 1e6, 1)}
 
 
 def unpack_int4(p):
@@ -213,7 +233,7 @@ def bench_w4a16(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int 
         sets.append((a, w, sc))
     a0, w0, s0 = sets[0]
     got = llmik.w4a16_gemm_f32out(a0, w0, s0, gs)
-    ref = a0.float() @ unpack_w4(w0).float().mul(s0.float().repeat_interleave(gs, dim=0))
+    ref = a0.double() @ unpack_w4(w0).double().mul(s0.double().repeat_interleave(gs, dim=0))
     err = gate(f"w4a16 M={M} K={K} N={N}", got, ref)
     del ref, got
     fns = [lambda s=s: llmik.w4a16_gemm(s[0], s[1], s[2], gs) for s in sets]
@@ -226,7 +246,8 @@ def bench_w4a16(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int 
     return {"name": "w4a16", "M": M, "K": K, "N": N, "us": round(us, 3), "bytes": nbytes,
             "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "TFLOPs": round(tf, 2), "frac_mfma_fp16_peak": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
-            "max_abs_err_f32out": err, "sets": n_sets}
+            "max_abs_err_f32out": err, "sets": n_sets,
+            "rotated_MB": round(n_sets * nbytes / 1e6, 1)}
 
 
 def bench_prefill(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int = 128,
@@ -461,113 +482,159 @@ def bench_append(llmik, B: int, S: int, steps: int, warmup: int, seed: int = 0):
 
 # -------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(budget_s: float = 15.0):
-    """Time the oracle's eager fp32 attention (reference form) on the host."""
-    import numpy as np
-    from oracle import attention as oa
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()
-                       if i.get("user_api") == "blas"), default=1)
-    except Exception:   # pragma: no cover
-        threads = os.cpu_count() or 1
-    rng = np.random.default_rng(0)
-    B, H, Hkv, S, D = 8, 32, 8, 4096, 128
-    q = rng.standard_normal((B, H, D)).astype(np.float16)
-    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
-    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
-    oa.decode_attention_expanded(q, k, v)        # warm-up
+def _timed_median(fn, budget_s: float, min_calls: int = 10, warmup: int = 3,
+                  max_calls: int = 50):
+    """Median microseconds of fn() after `warmup` calls: at least `min_calls`
+    calls, more while the budget lasts (at most `max_calls`)."""
+    for _ in range(warmup):
+        fn()
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
+    while len(times) < min_calls or (time.perf_counter() < t_end and len(times) < max_calls):
         t0 = time.perf_counter_ns()
-        oa.decode_attention_expanded(q, k, v)
-        times.append((time.perf_counter_ns() - t0) / 1e3)
-        if len(times) >= 50:
-            break
-    times.sort()
-    med = times[len(times) // 2]
-    return {"value": round(med, 1), "unit": "us", "cores": int(threads), "kind": "port",
-            "sample": f"{len(times)} full calls of oracle/attention.py decode_attention_expanded "
-                      f"(eager fp32, repeat_interleave GQA) at B=8 H=32 Hkv=8 D=128 S=4096, "
-                      f"median; numpy BLAS threads={threads}"}
-
-
-def cpu_details(budget_s: float = 4.0):
-    """The oracle's writers, W4A16 reference matmul and weight quantiser +
-    packer (reference forms: quantisers on x.float(), quantized_matmul_ref
-    with its per-call fp32 dequant) on the host, one config each, median of
-    the calls that fit in `budget_s` (at least 2)."""
-    import numpy as np
-    from oracle import kv_quant as okq
-    from oracle import w4a16 as ow
-    rng = np.random.default_rng(0)
-
-    def timed(fn):
         fn()
-        times, t_end = [], time.perf_counter() + budget_s
-        while time.perf_counter() < t_end or len(times) < 2:
-            t0 = time.perf_counter_ns()
-            fn()
-            times.append((time.perf_counter_ns() - t0) / 1e3)
-        times.sort()
-        return round(times[len(times) // 2], 1), len(times)
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+    times.sort()
+    return times[len(times) // 2], len(times)
 
+
+def cpu_baseline(budget_s: float = 12.0):
+    """The reference's eager fp32 decode attention (attention_ref.py:43-80,
+    restated with torch CPU ops in oracle/torch_ref.py) at the headline shape
+    on the host cores."""
+    import torch
+    from oracle import torch_ref as tr
+    threads = tr.host_threads()
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(0)
+    B, H, Hkv, S, D = 8, 32, 8, 4096, 128
+    q = torch.randn((B, H, D), generator=gen).half()
+    k = torch.randn((B, Hkv, S, D), generator=gen).half()
+    v = torch.randn((B, Hkv, S, D), generator=gen).half()
+    med, n = _timed_median(lambda: tr.eager_decode_attention(q, k, v, 1.0 / math.sqrt(D)), budget_s)
+    return {"value": round(med, 1), "unit": "us", "cores": threads, "kind": "port",
+            "sample": f"{n} full calls (after 3 warm-up) of oracle/torch_ref.py eager_decode_attention "
+                      f"(torch CPU: repeat_interleave GQA, fp32 matmul, softmax, matmul, .to(fp16)) "
+                      f"at B=8 H=32 Hkv=8 D=128 S=4096, median; torch.set_num_threads({threads}) "
+                      f"from os.sched_getaffinity capped by OMP_NUM_THREADS"}
+
+
+def cpu_details(budget_s: float = 3.0):
+    """The reference's other CPU paths restated with torch ops
+    (oracle/torch_ref.py): the KV quantisers on x.float() at B=8, S=4096,
+    quantized_matmul_ref (with its per-call fp32 dequant) at M=1 on the three
+    Llama shapes, and the numpy port of the attention for comparison; median
+    of >= 10 calls after 3 warm-up calls each."""
+    import numpy as np
+    import torch
+    from oracle import attention as oa
+    from oracle import torch_ref as tr
+    threads = tr.host_threads()
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(0)
     out = []
-    x = rng.standard_normal((8, 8, 4096, 128)).astype(np.float16).astype(np.float32)
-    for name, fn in (("quantize_per_token_int8", lambda: okq.quantize_per_token(x, 8)),
+    x = torch.randn((8, 8, 4096, 128), generator=gen).half().float()
+    for name, fn in (("quantize_per_token_int8", lambda: tr.quantize_per_token(x, 8)),
                      ("quantize_k_groupwise_int4_g128",
-                      lambda: okq.quantize_per_channel_groupwise(x, 4, 128)),
-                     ("quantize_v_per_token_int4", lambda: okq.quantize_per_token(x, 4))):
-        us, n = timed(fn)
-        out.append({"name": name, "B": 8, "S": 4096, "cpu_us": us, "calls": n})
+                      lambda: tr.quantize_per_channel_groupwise(x, 4, 128)),
+                     ("quantize_v_per_token_int4", lambda: tr.quantize_per_token(x, 4))):
+        us, n = _timed_median(fn, budget_s)
+        out.append({"name": name, "B": 8, "S": 4096, "cpu_us": round(us, 1), "calls": n,
+                    "cores": threads, "impl": "torch"})
     del x
     for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
-        W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
-        q, s = ow.quantize_weights_int4_groupwise(W, 128)
-        s = s.astype(np.float16)
-        del W
-        act = rng.standard_normal((1, K)).astype(np.float16)
-        us, n = timed(lambda: ow.quantized_matmul_ref(act, q, s, 128))
-        out.append({"name": "w4a16", "M": 1, "K": K, "N": N, "cpu_us": us, "calls": n})
-        del q, s
-    W = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
-
-    def quant_pack():
-        q, s = ow.quantize_weights_int4_groupwise(W, 128)
-        return ow.pack_int4_along_k(q), s.astype(np.float16)
-    us, n = timed(quant_pack)
-    out.append({"name": "w4_quantize_pack_fp32", "K": 4096, "N": 4096, "cpu_us": us, "calls": n})
-    del W
+        q = torch.randint(-7, 8, (K, N), generator=gen, dtype=torch.int8)
+        sc = (torch.rand((K // 128, N), generator=gen) * 0.004 + 0.001).half()
+        act = torch.randn((1, K), generator=gen).half()
+        us, n = _timed_median(lambda: tr.quantized_matmul_ref(act, q, sc, 128), budget_s)
+        out.append({"name": "w4a16", "M": 1, "K": K, "N": N, "cpu_us": round(us, 1), "calls": n,
+                    "cores": threads, "impl": "torch"})
+        del q, sc, act
+    rng = np.random.default_rng(0)
+    qn = rng.standard_normal((8, 32, 128)).astype(np.float16)
+    kn = rng.standard_normal((8, 8, 4096, 128)).astype(np.float16)
+    vn = rng.standard_normal((8, 8, 4096, 128)).astype(np.float16)
+    us, n = _timed_median(lambda: oa.decode_attention_expanded(qn, kn, vn), budget_s, min_calls=5)
+    out.append({"name": "attn_fp16", "B": 8, "S": 4096, "cpu_us": round(us, 1), "calls": n,
+                "impl": "numpy port (oracle/attention.py decode_attention_expanded)"})
     return out
 
 
 # ------------------------------------------------------------- HBM traffic
 
-def pmc_workload(llmik, steps: int) -> None:
-    """The program the rocprofv3 --pmc passes run: the headline attention
-    call `steps` times, eagerly, over rotating HBM-resident input sets, then
-    five plain copies of 256 MiB (torch copy_, a read and a write of known
-    size) whose counter readings give the scale factor."""
+PMC_WORKLOADS = ("attn:fp16", "attn:int8", "attn:int4", "attn:int4g32", "attn:int4b64",
+                 "w4a16:1", "w4a16:16", "w4a16:128")
+
+
+def pmc_workload(llmik, name: str, steps: int) -> None:
+    """The program the rocprofv3 --pmc passes run: `steps` eager calls of one
+    kernel family over rotating HBM-resident input sets (>= 768 MiB), then
+    five plain 256 MiB device copies (torch copy_, a read and a write of
+    known size) whose counter readings give the scale factor.
+
+      attn:fp16 / attn:int8 / attn:int4 / attn:int4g32   B=8, S=4096 (the
+          headline shape; INT4 at group 128 or 32, K with outlier channels)
+      attn:int4b64                     INT4 g128 at B=64, S=8192
+      w4a16:M                          M rows on (4096,4096), (4096,14336),
+                                       (14336,4096), `steps` calls each, in
+                                       that order
+    """
     import torch
     dev = torch.device("cuda:0")
-    B, H, Hkv, S, D = 8, 32, 8, 4096, 128
-    n_sets = n_sets_for(attn_bytes("fp16", B, H, Hkv, S, D))
     gen = torch.Generator(device=dev).manual_seed(1)
-    sets = [(torch.randn((B, H, D), generator=gen, device=dev, dtype=torch.float16),
-             torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16),
-             torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16))
-            for _ in range(n_sets)]
-    for i in range(steps):
-        llmik.decode_attention(*sets[i % n_sets], 1.0 / math.sqrt(D))
+    kind, arg = name.split(":")
+    if kind == "attn":
+        fmt = {"fp16": "fp16", "int8": "int8"}.get(arg, "int4")
+        gs = 32 if arg == "int4g32" else 128
+        B, S = (64, 8192) if arg == "int4b64" else (8, 4096)
+        H, Hkv, D = 32, 8, 128
+        n_sets = n_sets_for(attn_bytes(fmt, B, H, Hkv, S, D, gs))
+        calls = []
+        for _ in range(n_sets):
+            q = torch.randn((B, H, D), generator=gen, device=dev, dtype=torch.float16)
+            k = torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16)
+            v = torch.randn((B, Hkv, S, D), generator=gen, device=dev, dtype=torch.float16)
+            if fmt == "fp16":
+                calls.append(lambda q=q, k=k, v=v: llmik.decode_attention(q, k, v, D ** -0.5))
+                continue
+            k[..., [3, 37, 71, 105]] *= 10
+            if fmt == "int8":
+                t = (q, *llmik.quantize_per_token(k), *llmik.quantize_per_token(v))
+                calls.append(lambda t=t: llmik.decode_attention_int8(*t, D ** -0.5))
+            else:
+                t = (q, *llmik.quantize_k_per_channel_groupwise_int4(k, gs),
+                     *llmik.quantize_v_per_token_int4(v))
+                calls.append(lambda t=t: llmik.decode_attention_int4(*t, gs, D ** -0.5))
+            del k, v
+        torch.cuda.synchronize()
+        log(f"pmc workload {name}: B={B} S={S} {fmt}" + (f" g{gs}" if fmt == "int4" else "")
+            + f", {n_sets} input sets, {steps} calls")
+        for i in range(steps):
+            calls[i % n_sets]()
+    elif kind == "w4a16":
+        M = int(arg)
+        for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
+            n_sets = n_sets_for(w4a16_bytes(M, K, N))
+            sets = [(torch.randn((M, K), generator=gen, device=dev, dtype=torch.float16),
+                     torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), generator=gen, device=dev,
+                                   dtype=torch.int32),
+                     (torch.rand((K // 128, N), generator=gen, device=dev) * 0.004 + 0.001).half())
+                    for _ in range(n_sets)]
+            torch.cuda.synchronize()
+            log(f"pmc workload {name}: M={M} K={K} N={N}, {n_sets} input sets, {steps} calls")
+            for i in range(steps):
+                llmik.w4a16_gemm(*sets[i % n_sets], 128)
+            torch.cuda.synchronize()
+            del sets
+    else:
+        raise SystemExit(f"unknown --pmc-workload {name}; one of {PMC_WORKLOADS}")
     torch.cuda.synchronize()
-    del sets
     src = torch.randint(0, 255, (256 << 20,), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"pmc workload done: {steps} attention calls (B={B} S={S}), 5 x 256 MiB copies")
+    log(f"pmc workload {name} done; 5 x 256 MiB copies")
 
 
 def read_traffic():
@@ -597,8 +664,10 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list: int8,int4,w4a16,prefill,layer,writers,append,sweep,wquant")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="run the counter-collection program (headline calls + copies) and exit")
+    ap.add_argument("--pmc-workload", nargs="?", const="attn:fp16", default=None,
+                    choices=PMC_WORKLOADS,
+                    help="run a counter-collection program (one kernel family's calls, then "
+                         "calibration copies) and exit; default attn:fp16, the headline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are out of scope "
@@ -611,14 +680,15 @@ def main() -> None:
         raise SystemExit("bench.py needs a GPU")
     log(f"device {torch.cuda.get_device_name(0)}; library {llmik.LIB_PATH}")
     if args.pmc_workload:
-        pmc_workload(llmik, args.steps)
+        pmc_workload(llmik, args.pmc_workload, args.steps)
         return
 
     only = set(filter(None, args.only.split(",")))
     want = (lambda k: not only or k in only)
 
     t_wall = time.perf_counter()
-    head = bench_attention(llmik, "fp16", 8, 4096, args.steps, args.warmup, seed=1)
+    head = bench_attention(llmik, "fp16", 8, 4096, args.steps, args.warmup, seed=1,
+                           exact_steps=True)
     log(f"headline {head}")
     details = []
     if not args.no_details:
@@ -630,6 +700,9 @@ def main() -> None:
                 details.append(bench_attention(llmik, "int4", B, S, 100 if B == 8 else 30, 10,
                                                gs=128, seed=3))
                 log(details[-1])
+            # group 32: the integration's default (integration/kv_int4_cache.py:73)
+            details.append(bench_attention(llmik, "int4", 8, 4096, 100, 10, gs=32, seed=3))
+            log(details[-1])
             details.append(bench_attention(llmik, "fp16", 64, 8192, 20, 5, seed=4))
             log(details[-1])
         if want("sweep"):

@@ -22,7 +22,9 @@
 //   QK : A = q (16 rows, row m holds head m % HPW), B = 16 tokens' keys
 //        (lane = token, 8 consecutive channels per lane group) -> every lane
 //        gets the scores of its token for all heads; no lane reductions.
-//   PV : A = p (fp16, through a 256-byte per-wave LDS slot), B = values:
+//   PV : A = p as an fp16 hi + lo pair (two MFMAs per B operand, through a
+//        512-byte per-wave LDS slot; fp16 p alone would cost ~2^-12 |v| of
+//        accuracy under a peaked softmax), B = values:
 //        lane (g, c) loads the channels 8c..8c+7 of tokens 8g..8g+7 (full
 //        cache rows per load instruction) and one v_perm_b32 per dword turns
 //        them into the B operand of MFMA j, which owns channels 8c + j.
@@ -411,20 +413,24 @@ struct MfmaTile<KvFormat::I4> {
         return as_f16x8(make_u32x4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
                                    __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)));
     }
-    // B operand of PV MFMA j, biased: even j takes the low nibbles (channel
-    // 8c + j even) as 1024 + (code + 8) = code + 1032, odd j the high nibbles
-    // as 1024 + 16 (code + 8) = 16 code + 1152. The bias and the factor 16
-    // are taken out once, at the end, from the sum of P (kVBias, kVUnscale).
-    static constexpr float kVBias[2] = {1032.0f, 1152.0f};
-    static constexpr float kVUnscale[2] = {1.0f, 0.0625f};
+    // B operand of PV MFMA j, biased: every code enters as the exact fp16
+    // 1024 + 16 (code + 8) = 16 code + 1152, its nibble in mantissa bits 4-7.
+    // Odd j (channel 8c + j odd) takes the high nibbles in place; even j the
+    // low nibbles of the words shifted left by 4 (vop_lo). The bias and the
+    // factor 16 are taken out once, at the end, from the sum of P (kVBias,
+    // kVUnscale). A low nibble in bits 0-3 (1024 + code + 8) would put ~130x
+    // the signal into the fp32 accumulator as bias, against ~9x here.
+    static constexpr float kVBias[2] = {1152.0f, 1152.0f};
+    static constexpr float kVUnscale[2] = {0.0625f, 0.0625f};
     __device__ __forceinline__ f16x8 vop(const TileCtx& x, int j) const {
         const int byte = j >> 1;
         const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
         uint32_t d[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t xw = perm_b32(v[2 * i + 1], v[2 * i], sel);
-            d[i] = (j & 1) ? ((xw & x.m_hi) ^ x.x_hi) : ((xw & x.m_lo) ^ x.x_lo);
+            const uint32_t lo = (j & 1) ? v[2 * i] : (v[2 * i] << 4);
+            const uint32_t hi = (j & 1) ? v[2 * i + 1] : (v[2 * i + 1] << 4);
+            d[i] = (perm_b32(hi, lo, sel) & x.m_hi) ^ x.x_hi;
         }
         return as_f16x8(make_u32x4(d[0], d[1], d[2], d[3]));
     }
@@ -482,7 +488,9 @@ void decode_attention_mfma_kernel(AttnParams p) {
         l[i] = 0.0f;
     }
 
-    __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][4][kTile];
+    // P as an fp16 hi + lo pair (plane 0: fp16(x), plane 1: fp16(x - hi)),
+    // so that the PV products carry p to ~2^-22 instead of fp16's 2^-12.
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][2][4][kTile];
 
     const int t_begin = split * p.chunk;
     const int t_end = min(t_begin + p.chunk, p.seqlen);
@@ -607,20 +615,34 @@ void decode_attention_mfma_kernel(AttnParams p) {
                 f0 *= h2f(tile.vs[0]);
                 f1 *= h2f(tile.vs[1]);
             }
-            s_p[wave][g][c] = f2h_bits(pr[0][g] * f0);
-            s_p[wave][g][16 + c] = f2h_bits(pr[1][g] * f1);
+            // x - fp16(x) is exact in fp32; rounding it to fp16 leaves a
+            // relative error of 2^-11 of a term that is itself <= 2^-11 x.
+            const float x0 = pr[0][g] * f0, x1 = pr[1][g] * f1;
+            const uint16_t h0 = f2h_bits(x0), h1 = f2h_bits(x1);
+            s_p[wave][0][g][c] = h0;
+            s_p[wave][0][g][16 + c] = h1;
+            s_p[wave][1][g][c] = f2h_bits(x0 - h2f(h0));
+            s_p[wave][1][g][16 + c] = f2h_bits(x1 - h2f(h1));
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const f16x8 pa = as_f16x8(load16(&s_p[wave][c % HPW][8 * g]));
+        const f16x8 pa = as_f16x8(load16(&s_p[wave][0][c % HPW][8 * g]));
+        const f16x8 pl = as_f16x8(load16(&s_p[wave][1][c % HPW][8 * g]));
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
 
-        // ---- O += P V ----
+        // ---- O += P V (hi and lo parts of P against the same B operand) ----
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = mfma16x16x32(pa, tile.vop(x, j), o[j]);
-        if constexpr (F != KvFormat::F16) sum_p = mfma16x16x32(pa, ones, sum_p);
+        for (int j = 0; j < 8; ++j) {
+            const f16x8 vb = tile.vop(x, j);
+            o[j] = mfma16x16x32(pa, vb, o[j]);
+            o[j] = mfma16x16x32(pl, vb, o[j]);
+        }
+        if constexpr (F != KvFormat::F16) {
+            sum_p = mfma16x16x32(pa, ones, sum_p);
+            sum_p = mfma16x16x32(pl, ones, sum_p);
+        }
     };
 
     auto load_tile = [&](MfmaTile<F>& t, int t0) {

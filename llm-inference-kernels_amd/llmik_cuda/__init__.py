@@ -28,7 +28,7 @@ the reference):
 """
 from __future__ import annotations
 
-from typing import Dict, Tuple
+from typing import Dict, List, Tuple
 
 import torch
 
@@ -62,6 +62,11 @@ def _stream(t: torch.Tensor) -> int:
 # completion counters at the start of a workspace zeroed, so a workspace is
 # reused by later calls on the same stream (stream order serialises them).
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+# Buffers replaced by a larger one. A HIP graph captured on a stream keeps the
+# address of the workspace it was captured with, and replays keep writing
+# partials and counters there, so a replaced buffer is never freed (the
+# doubling growth bounds what is held to twice the largest workspace).
+_RETIRED_WORKSPACES: List[torch.Tensor] = []
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> Tuple[int, int]:
@@ -71,6 +76,8 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> Tuple[int, int
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes, 2 * ws.numel() if ws is not None else 0)
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
         ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws.data_ptr(), ws.numel()

@@ -22,5 +22,9 @@ Pinning (what fixes each function independently of its own formulas):
                                                      -> tests/test_oracle_w4a16.py
   fused       closed forms (unit weight / zero input) and the reference
               test's PyTorch formulas                -> tests/test_oracle_fused.py
+  torch_ref   the same reference paths as torch CPU ops (the host baseline
+              bench.py times), pinned to the numpy functions above
+                                                     -> tests/test_oracle_torch_ref.py
 """
 from . import attention, fused, kv_quant, w4a16  # noqa: F401
+# torch_ref (torch CPU restatements for the host baseline) is imported on demand.

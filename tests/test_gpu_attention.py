@@ -157,3 +157,117 @@ def test_int4_large_batch_config_properties(llmik, cuda):
                                         ks[perm].contiguous(), vq_[perm].contiguous(),
                                         vs[perm].contiguous(), gs, 1 / math.sqrt(128))
     assert torch.equal(out_p, out[perm])
+
+
+def _sampled_rows_parity(out, q, k_rows, v_rows, rows, scale):
+    """Oracle parity on the sampled batch rows (the oracle runs per row, in
+    float64); k_rows / v_rows give the dequantised [1, Hkv, S, D] of a row."""
+    for b in rows:
+        ref = oa.decode_attention(q[b:b + 1], k_rows(b), v_rows(b), scale, acc_dtype=np.float64)
+        assert _max_abs(out[b:b + 1], ref) <= TOL, f"batch row {b}"
+
+
+@pytest.mark.parametrize("B,L", [(8, 32768), (64, 4096)])
+def test_fp16_swept_baseline_configs(llmik, cuda, B, L):
+    """The fp16 sweep configs of the headline shape: B=8, S=32768 (the
+    longest chunks) and B=64, S=4096 (4-wave workgroups, 512 of them, no
+    split). Oracle parity on sampled batch rows and a batch permutation that
+    must permute the outputs bit for bit."""
+    gen = torch.Generator(device=cuda).manual_seed(B + L)
+    kd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    vd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    q = randn((B, 32, 128), B * 7 + L).astype(np.float16)
+    qd = _dev(q, cuda)
+    scale = 1 / math.sqrt(128)
+    out = llmik.decode_attention(qd, kd, vd, scale)
+    _sampled_rows_parity(out, q, lambda b: kd[b:b + 1].cpu().numpy(),
+                         lambda b: vd[b:b + 1].cpu().numpy(), (0, B // 2 - 1, B - 1), scale)
+    perm = torch.randperm(B, generator=torch.Generator().manual_seed(1)).to(cuda)
+    out_p = llmik.decode_attention(qd[perm].contiguous(), kd[perm].contiguous(),
+                                   vd[perm].contiguous(), scale)
+    assert torch.equal(out_p, out[perm])
+
+
+def _peaked_inputs(B, L, seed):
+    """q heads of a kv group share one direction; three tokens of each (b, kv
+    head) have keys along it (scores ~12 against ~N(0,1) for the rest), so
+    ~95 % of the softmax mass sits on 2-3 near-equal tokens. V has three
+    channels x8 (|v| up to ~30)."""
+    rng = np.random.default_rng(seed)
+    Hkv, G, D = 8, 4, 128
+    base = rng.standard_normal((B, Hkv, 1, D))
+    q = (base + 0.05 * rng.standard_normal((B, Hkv, G, D))).reshape(B, Hkv * G, D)
+    k = rng.standard_normal((B, Hkv, L, D))
+    unit = base[:, :, 0] / np.linalg.norm(base[:, :, 0], axis=-1, keepdims=True)
+    peaks = (L // 7, L // 2 + 3, L - 2)
+    for i, t in enumerate(peaks):
+        k[:, :, t] = unit * math.sqrt(D) * (1.05 + 0.002 * i)
+    v = rng.standard_normal((B, Hkv, L, D))
+    v[..., [5, 50, 90]] *= 8.0
+    return q.astype(np.float16), k.astype(np.float16), v.astype(np.float16)
+
+
+def _half_ulp_f16(x: np.ndarray) -> np.ndarray:
+    """Half the fp16 spacing at |x| (the output's own rounding)."""
+    a = np.abs(x).astype(np.float16)
+    return (np.spacing(a).astype(np.float64)) / 2.0
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int8", "int4"])
+@pytest.mark.parametrize("B,L", [(2, 4096), (8, 1024)])
+def test_peaked_softmax_large_v_precision(llmik, cuda, fmt, B, L):
+    """Large-magnitude V under a peaked softmax, all three KV formats: the
+    error before the output's fp16 rounding must stay within 2e-3 of the
+    float64 attention over the (dequantised) cache, as the reference's fp32
+    P does (reference/attention_ref.py:71-80). Rounding P itself to fp16
+    would cost ~2^-12 * |v| (~7e-3 here)."""
+    q, k, v = _peaked_inputs(B, L, seed=B * 31 + L)
+    scale = 1 / math.sqrt(128)
+    qd, kd, vd = _dev(q, cuda), _dev(k, cuda), _dev(v, cuda)
+    if fmt == "fp16":
+        out = llmik.decode_attention(qd, kd, vd, scale)
+        k_dq, v_dq = k, v
+    elif fmt == "int8":
+        kq_, ks = llmik.quantize_per_token(kd)
+        vq_, vs = llmik.quantize_per_token(vd)
+        out = llmik.decode_attention_int8(qd, kq_, ks, vq_, vs, scale)
+        k_dq = kq.dequantize_per_token(kq_.cpu().numpy(), ks.cpu().numpy())
+        v_dq = kq.dequantize_per_token(vq_.cpu().numpy(), vs.cpu().numpy())
+    else:
+        gs = 32
+        kq_, ks = llmik.quantize_k_per_channel_groupwise_int4(kd, gs)
+        vq_, vs = llmik.quantize_v_per_token_int4(vd)
+        out = llmik.decode_attention_int4(qd, kq_, ks, vq_, vs, gs, scale)
+        k_dq = kq.dequantize_per_channel_groupwise(kq.unpack_kv_int4(kq_.cpu().numpy()),
+                                                   ks.cpu().numpy(), gs)
+        v_dq = kq.dequantize_per_token(kq.unpack_kv_int4(vq_.cpu().numpy()), vs.cpu().numpy())
+    ref = oa.decode_attention(q, k_dq, v_dq, scale, acc_dtype=np.float64)
+    assert np.abs(ref).max() > 8.0, "the case must produce large outputs"
+    err = np.abs(out.double().cpu().numpy() - ref) - _half_ulp_f16(ref)
+    assert float(err.max()) <= TOL
+
+
+def test_int4_long_unsplit_large_v(llmik, cuda):
+    """INT4 at B=64, S=8192 runs without splits (2048 tokens per wave), so each
+    wave's PV accumulator sums 64 tiles. V has three channels x8: the error
+    before output rounding stays within 2e-3 of float64 attention (a biased V
+    operand whose bias dwarfs the codes would lose ~2e-3 here)."""
+    B, L, gs = 64, 8192, 128
+    gen = torch.Generator(device=cuda).manual_seed(640)
+    kd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    kd[..., [3, 37, 71, 105]] *= 10
+    vd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    vd[..., [5, 50, 90]] *= 8
+    kq_, ks = llmik.quantize_k_per_channel_groupwise_int4(kd, gs)
+    vq_, vs = llmik.quantize_v_per_token_int4(vd)
+    del kd, vd
+    q = randn((B, 32, 128), 641).astype(np.float16)
+    out = llmik.decode_attention_int4(_dev(q, cuda), kq_, ks, vq_, vs, gs, 1 / math.sqrt(128))
+    for b in (0, 63):
+        k_dq = kq.dequantize_per_channel_groupwise(
+            kq.unpack_kv_int4(kq_[b:b + 1].cpu().numpy()), ks[b:b + 1].cpu().numpy(), gs)
+        v_dq = kq.dequantize_per_token(kq.unpack_kv_int4(vq_[b:b + 1].cpu().numpy()),
+                                       vs[b:b + 1].cpu().numpy())
+        ref = oa.decode_attention(q[b:b + 1], k_dq, v_dq, 1 / math.sqrt(128), acc_dtype=np.float64)
+        err = np.abs(out[b:b + 1].double().cpu().numpy() - ref) - _half_ulp_f16(ref)
+        assert float(err.max()) <= TOL, f"batch row {b}"

@@ -83,3 +83,44 @@ def test_split_handoff_is_deterministic(llmik, cuda, B, S):
     sc = (torch.rand((32, 4096), generator=gen, device=cuda) * 0.01).half()
     g0 = llmik.w4a16_gemm_f32out(act, w, sc, 128)
     assert all(torch.equal(g0, llmik.w4a16_gemm_f32out(act, w, sc, 128)) for _ in range(40))
+
+
+def test_graph_keeps_its_workspace_after_the_stream_grows(llmik, cuda):
+    """A graph captured with a small workspace on a stream, then a larger call
+    on the same stream that replaces that stream's workspace: the graph's
+    replays still use the buffer they were captured with, which must stay
+    allocated, and their outputs must equal the eager call bit for bit while
+    the caching allocator hands the freed-looking memory to other tensors."""
+    gen = torch.Generator(device=cuda).manual_seed(11)
+    q = torch.randn((1, 32, 128), generator=gen, device=cuda, dtype=torch.float16)
+    k = torch.randn((1, 8, 2048, 128), generator=gen, device=cuda, dtype=torch.float16)
+    v = torch.randn((1, 8, 2048, 128), generator=gen, device=cuda, dtype=torch.float16)
+    kb = torch.randn((4, 8, 32768, 128), generator=gen, device=cuda, dtype=torch.float16)
+    qb = torch.randn((4, 32, 128), generator=gen, device=cuda, dtype=torch.float16)
+    torch.cuda.synchronize()   # the inputs are written on the default stream
+    stream = torch.cuda.Stream(device=cuda)
+    with torch.cuda.stream(stream):
+        eager = llmik.decode_attention(q, k, v, 0.0883883)   # sizes this stream's workspace
+    stream.synchronize()
+    key = (cuda.index or 0, stream.cuda_stream)
+    small = llmik._WORKSPACES[key].data_ptr()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = llmik.decode_attention(q, k, v, 0.0883883)
+    # A call with more slot groups grows the same stream's workspace.
+    with torch.cuda.stream(stream):
+        big = llmik.decode_attention(qb, kb, kb, 0.0883883)
+    stream.synchronize()
+    assert llmik._WORKSPACES[key].data_ptr() != small, "the test must force a workspace growth"
+    # Fresh allocations that could land on a freed workspace, filled with garbage.
+    junk = [torch.full((1 << 20,), 7, dtype=torch.uint8, device=cuda) for _ in range(8)]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        with torch.cuda.stream(stream):
+            graph.replay()
+        stream.synchronize()
+        assert torch.equal(out, eager)
+        assert all(int((j != 7).count_nonzero()) == 0 for j in junk)
+    with torch.cuda.stream(stream):
+        assert torch.equal(llmik.decode_attention(qb, kb, kb, 0.0883883), big)
+    torch.cuda.synchronize()
