@@ -113,6 +113,23 @@ LLMIK_API llmik_status llmik_decode_attention_int4(
     int group_size, int n_groups, float softmax_scale, void* workspace, size_t workspace_bytes,
     void* stream);
 
+/*
+ * The same fp16 decode attention with no workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The split-K counters and partials live in a static device
+ * array of LLMIK_NOALLOC_SCRATCH_BYTES per device (held until the process
+ * ends); a call whose plan needs more (llmik_attention_workspace_size)
+ * returns LLMIK_ERR_WORKSPACE. It calls no allocator. All calls on one device
+ * share that array: calls that overlap on a device race, so issue them in
+ * one stream order. Results are bit-identical to llmik_decode_attention_f16.
+ */
+#define LLMIK_NOALLOC_SCRATCH_BYTES (2u << 20)
+LLMIK_API llmik_status llmik_decode_attention_f16_noalloc(
+    const void* q, const void* k, const void* v, void* out,
+    int batch, int n_heads, int n_kv_heads, int seqlen, int head_dim, int kv_buf_len,
+    float softmax_scale, void* stream);
+
 /* --------------------------------------------------------------- KV writers
  * Bit-exact symmetric quantisers: scale = max(absmax/qmax, 1e-8) in fp32
  * with IEEE division, q = clamp(round_half_even(x / scale), -qmax, qmax),

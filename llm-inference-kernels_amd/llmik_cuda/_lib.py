@@ -32,6 +32,7 @@ _SIGNATURES = {
     "llmik_abi_version": (_i, []),
     "llmik_attention_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
     "llmik_decode_attention_f16": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p]),
+    "llmik_decode_attention_f16_noalloc": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p]),
     "llmik_decode_attention_int8": (
         _i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p]),
     "llmik_decode_attention_int4": (
