@@ -257,6 +257,17 @@ LLMIK_API llmik_status llmik_w4a16_gemm_f32out(
     int M, int N, int K, int group_size, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Plan knobs of the W4A16 entry points, for measurement and tests (no
+ * reference counterpart). stream_mode: 1 forces the streaming GEMV wherever
+ * the shape allows, 0 disables it, -1 restores the size rule; stream_splits
+ * > 0 forces its K split count, <= 0 restores the planner's. The library
+ * reads the initial values once, when it loads, from LLMIK_W4A16_STREAM and
+ * LLMIK_W4A16_STREAM_SPLITS. Not synchronised with calls in flight on other
+ * threads.
+ */
+LLMIK_API void llmik_w4a16_set_plan_override(int stream_mode, int stream_splits);
+
+/*
  * Materialise fp16 W[k, n] = fp16(q[k, n] * scale[k/g, n]).
  * Replaces: w4a16_dequantize op (bindings/extension.cpp:382-403) and
  *   launch_w4a16_dequantize (kernels/quant/quant_matmul.cuh:58-60;

@@ -329,6 +329,10 @@ LLMIK_API llmik_status llmik_w4a16_gemm_f32out(const void* act, const void* weig
                         workspace_bytes, as_stream(stream));
 }
 
+LLMIK_API void llmik_w4a16_set_plan_override(int stream_mode, int stream_splits) {
+    set_w4a16_plan_override(stream_mode, stream_splits);
+}
+
 LLMIK_API llmik_status llmik_w4a16_dequantize(const void* weight_packed, const void* scale,
                                               void* out, int K, int N, int group_size,
                                               void* stream) {

@@ -14,6 +14,9 @@
 // order and writes the output. One launch per call, no float atomics (the
 // reference accumulates split partials with atomicAdd,
 // kernels/quant/quant_matmul.cu:586-597).
+#include <atomic>
+#include <cstdlib>
+
 #include "device_common.hpp"
 #include "llmik_internal.hpp"
 
@@ -1695,24 +1698,33 @@ __global__ __launch_bounds__(256) void w4a16_dequantize_kernel(const uint32_t* _
 // Host side
 // ---------------------------------------------------------------------------
 
-// Streaming GEMV selection: "1" forces it wherever the shape allows, "0"
-// disables it; unset, it serves weights of at least kStreamMinWeightBytes
-// (below that the single-row / 16-row GEMVs with 32-column tiles have less
-// fixed cost per call).
+// Streaming GEMV selection: 1 forces it wherever the shape allows, 0
+// disables it; unset (-1), it serves weights of at least
+// kStreamMinWeightBytes (below that the single-row / 16-row GEMVs with
+// 32-column tiles have less fixed cost per call). A positive split count
+// forces the streaming GEMV's K split count (clamped to what the K extent
+// allows). Both are measurement knobs: read once from LLMIK_W4A16_STREAM /
+// LLMIK_W4A16_STREAM_SPLITS when the library loads, and settable with
+// llmik_w4a16_set_plan_override.
 constexpr long kStreamMinWeightBytes = 16L << 20;
 
-static int stream_override() {
-    const char* e = getenv("LLMIK_W4A16_STREAM");
+namespace {
+int env_int(const char* name, bool as_flag) {
+    const char* e = getenv(name);
     if (e == nullptr || *e == '\0') return -1;
-    return (*e == '0') ? 0 : 1;
+    return as_flag ? ((*e == '0') ? 0 : 1) : atoi(e);
+}
+std::atomic<int> g_stream_mode{env_int("LLMIK_W4A16_STREAM", true)};
+std::atomic<int> g_stream_splits{env_int("LLMIK_W4A16_STREAM_SPLITS", false)};
+}  // namespace
+
+void set_w4a16_plan_override(int stream_mode, int stream_splits) {
+    g_stream_mode.store(stream_mode < 0 ? -1 : (stream_mode ? 1 : 0), std::memory_order_relaxed);
+    g_stream_splits.store(stream_splits > 0 ? stream_splits : -1, std::memory_order_relaxed);
 }
 
-// LLMIK_W4A16_STREAM_SPLITS=n forces the streaming GEMV's K split count
-// (clamped to what the K extent allows), for measurement.
-static int stream_splits_override() {
-    const char* e = getenv("LLMIK_W4A16_STREAM_SPLITS");
-    return (e == nullptr || *e == '\0') ? -1 : atoi(e);
-}
+static int stream_override() { return g_stream_mode.load(std::memory_order_relaxed); }
+static int stream_splits_override() { return g_stream_splits.load(std::memory_order_relaxed); }
 
 GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     GemmPlan pl{};

@@ -26,7 +26,7 @@ un-expanded [B, Hkv, S, D]. This module plugs into that registry:
   prefill sees the reference's fp16 view (dequantised full groups plus the
   fp16 tokens of the open group, kv_int4_cache.py:225-245); decode sees the
   packed buffers.
-* ``QuantizedLinear`` / ``patch_model_w4a16``: integration/w4a16_patch.py:45-174
+* ``QuantizedLinear`` / ``patch_model_w4a16``: integration/w4a16_patch.py:56-174
   (W4A16 projections; the GEMM below 256 rows, dequantise + matmul above),
   with the weights quantised on the GPU (quantize_pack_weights_int4, the
   same bits as the reference's torch quantiser).
@@ -262,7 +262,7 @@ _TARGET_LINEAR_NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "up_proj", "gate
 
 
 class QuantizedLinear(nn.Module):
-    """W4A16 replacement for nn.Linear(bias=False) (integration/w4a16_patch.py:45-136):
+    """W4A16 replacement for nn.Linear(bias=False) (integration/w4a16_patch.py:56-141):
     packed INT4 weights [K/8, N] int32 and fp16 scales [K/g, N]; forward runs
     w4a16_gemm below 256 rows and dequantise + matmul above."""
 
@@ -296,7 +296,7 @@ class QuantizedLinear(nn.Module):
 def patch_model_w4a16(model: nn.Module, *, group_size: int = 128) -> int:
     """Replace each bias-free q/k/v/o/gate/up/down projection Linear of
     model.model.layers with a QuantizedLinear (one-way, as the reference's
-    patch_model_w4a16, w4a16_patch.py:138-174). Returns the count."""
+    patch_model_w4a16, w4a16_patch.py:143-174). Returns the count."""
     replaced = 0
     for layer in model.model.layers:
         for parent_name in ("self_attn", "mlp"):

@@ -7,10 +7,10 @@ two-stage LDS reduction with and without a partner wave); one split and
 several, with a short last split and waves past the end of the K range;
 scale groups of 32..512 (a flush per group, or per batch inside a longer
 group); M = 1 and 2..16; more tiles than CUs (a second round of
-workgroups); and split counts forced with LLMIK_W4A16_STREAM_SPLITS.
+workgroups); and split counts forced with llmik_w4a16_set_plan_override.
 
 The library serves these shapes with the streaming kernel when the packed
-weights reach 16 MiB; the tests set LLMIK_W4A16_STREAM=1 so that the small
+weights reach 16 MiB; the tests force it (llmik_w4a16_set_plan_override) so that the small
 shapes take it too. Every packed word is random (every code -8..7 occurs),
 scales are random positive fp16, and the reference is act @ (code * scale)
 accumulated in float64 on the GPU in K chunks. Gate (written here): the
@@ -67,11 +67,19 @@ def _ref(act: torch.Tensor, w: torch.Tensor, sc: torch.Tensor, gs: int) -> torch
     return out
 
 
+def _set_plan(stream_mode: int, splits: int) -> None:
+    from llmik_cuda._lib import lib
+    lib.llmik_w4a16_set_plan_override(stream_mode, splits)
+
+
 @pytest.fixture(autouse=True)
-def _force_stream(monkeypatch):
+def _force_stream(llmik):
     """Route every eligible shape to the streaming kernel (the library
-    otherwise keeps it for weights of 16 MiB and more)."""
-    monkeypatch.setenv("LLMIK_W4A16_STREAM", "1")
+    otherwise keeps it for weights of 16 MiB and more); restore the planner
+    afterwards."""
+    _set_plan(1, -1)
+    yield
+    _set_plan(-1, -1)
 
 
 @pytest.mark.parametrize("M,K,N,gs", CASES)
@@ -90,10 +98,10 @@ def test_stream_gemv(llmik, cuda, M, K, N, gs):
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 5, 8])
-def test_stream_forced_splits(llmik, cuda, monkeypatch, splits):
-    """LLMIK_W4A16_STREAM_SPLITS forces the K split count; every count gives
-    results within the gate, and the same fp16 bits as its own fp32 call."""
-    monkeypatch.setenv("LLMIK_W4A16_STREAM_SPLITS", str(splits))
+def test_stream_forced_splits(llmik, cuda, splits):
+    """A forced K split count (llmik_w4a16_set_plan_override); every count
+    gives results within the gate, and the same fp16 bits as its own fp32 call."""
+    _set_plan(1, splits)
     test_stream_gemv(llmik, cuda, 8, 4096, 6144, 128)
     test_stream_gemv(llmik, cuda, 1, 4096, 28672, 128)
 
