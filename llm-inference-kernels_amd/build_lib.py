@@ -73,11 +73,42 @@ def build(jobs: int = 8) -> Path:
     return out
 
 
+TORCH_SRC = PKG_ROOT / "csrc_torch" / "torch_ops.cpp"
+
+
+def build_torch_ext() -> Path:
+    """Compile llmik_cuda/_C (csrc_torch/torch_ops.cpp, the torch-facing
+    validation / allocation / stream half of the ops) with the host C++
+    compiler against torch's headers, linked to libllmik_hip.so (found next
+    to it through an $ORIGIN rpath)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as ce
+    cxx = os.environ.get("CXX", "g++")
+    out = OUT_DIR / ("_C" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_suffix(".tmp")
+    inc = [*ce.include_paths(), sysconfig.get_paths()["include"], "/opt/rocm/include"]
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=_C",
+           "-DTORCH_API_INCLUDE_EXTENSION_H",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-I{d}" for d in inc], str(TORCH_SRC), "-o", str(tmp),
+           *[f"-L{d}" for d in ce.library_paths()], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", f"-L{OUT_DIR}", "-lllmik_hip", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch extension build failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
     args = ap.parse_args()
     print(build(args.jobs))
+    print(build_torch_ext())
 
 
 if __name__ == "__main__":
