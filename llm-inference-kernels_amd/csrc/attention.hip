@@ -455,7 +455,10 @@ void decode_attention_mfma_kernel(AttnParams p) {
     const int c = lane & 15;
 
     const int head0 = kvh * p.gqa + hchunk * HPW;
-    const uint16_t* qrow = p.q + ((long)b * p.n_heads + head0 + (c % HPW)) * kHeadDim;
+    // QK's A operand row m holds head (m / 4) % HPW: the four outputs of lane
+    // group g (rows 4g..4g+3) are all head g % HPW's scores, so each lane
+    // group runs the online softmax of one head (PV keeps row m = head m % HPW).
+    const uint16_t* qrow = p.q + ((long)b * p.n_heads + head0 + ((c >> 2) % HPW)) * kHeadDim;
 
     // Q as the A operand (4 k-steps); for INT4 the hi/lo pair of q * k_scale.
     f16x8 qa[4], qlo[4];
@@ -481,16 +484,15 @@ void decode_attention_mfma_kernel(AttnParams p) {
     // once at the end: o_j = (o_j - kVBias * sum_p) * kVUnscale.
     f32x4 sum_p = {0.0f, 0.0f, 0.0f, 0.0f};
     const f16x8 ones = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
-    float m[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m[i] = -INFINITY;
-        l[i] = 0.0f;
-    }
+    // Online-softmax state of this lane group's head (the same in its 16 lanes).
+    float m_run = -INFINITY, l_run = 0.0f;
 
     // P as an fp16 hi + lo pair (plane 0: fp16(x), plane 1: fp16(x - hi)),
     // so that the PV products carry p to ~2^-22 instead of fp16's 2^-12.
     __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][2][4][kTile];
+    // Each head's rescale factor of the tile, for the PV accumulators, which
+    // hold all heads in every lane.
+    __shared__ __attribute__((aligned(16))) float s_alpha[NW][4];
 
     const int t_begin = split * p.chunk;
     const int t_end = min(t_begin + p.chunk, p.seqlen);
@@ -549,7 +551,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
     auto step = [&](const MfmaTile<F>& tile, const int t0) {
 
         // ---- scores for the tile's two 16-token blocks ----
-        float s[2][4];
+        float s[2];
         if constexpr (F == KvFormat::I4) {
             if (tile.grp != cur_group) {   // wave-uniform; the scales came with the tile
                 cur_group = tile.grp;
@@ -577,38 +579,21 @@ void decode_attention_mfma_kernel(AttnParams p) {
             const bool valid = (t0 + 16 * blk + c) < w1;
             float sc = p.scale_log2;
             if constexpr (F == KvFormat::I8) sc *= h2f(tile.ks[blk]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s[blk][i] = valid ? acc[i] * sc : -INFINITY;
+            s[blk] = valid ? acc[0] * sc : -INFINITY;
         }
 
-        // ---- online softmax over the 32 tokens (identical in all 4 lane groups) ----
-        float pr[2][4];
-        bool rescale = false;
-        float alpha[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float tmax = row16_max(fmaxf(s[0][i], s[1][i]));
-            const float mn = fmaxf(m[i], tmax);
-            const float msafe = (mn == -INFINITY) ? 0.0f : mn;
-            alpha[i] = __builtin_amdgcn_exp2f(m[i] - msafe);
-            rescale |= (mn != m[i]);
-            m[i] = mn;
-            pr[0][i] = __builtin_amdgcn_exp2f(s[0][i] - msafe);
-            pr[1][i] = __builtin_amdgcn_exp2f(s[1][i] - msafe);
-            l[i] = fmaf(l[i], alpha[i], pr[0][i] + pr[1][i]);
-        }
-        if (rescale) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) o[j][i] *= alpha[i];
-            if constexpr (F != KvFormat::F16) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) sum_p[i] *= alpha[i];
-            }
-        }
+        // ---- online softmax of lane group g's head over the 32 tokens ----
+        const float tmax = row16_max(fmaxf(s[0], s[1]));
+        const float mn = fmaxf(m_run, tmax);
+        const float msafe = (mn == -INFINITY) ? 0.0f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - msafe);
+        const bool rescale = __builtin_amdgcn_ballot_w64(mn != m_run) != 0;   // wave-uniform
+        m_run = mn;
+        const float pr0 = __builtin_amdgcn_exp2f(s[0] - msafe);
+        const float pr1 = __builtin_amdgcn_exp2f(s[1] - msafe);
+        l_run = fmaf(l_run, alpha, pr0 + pr1);
 
-        // ---- p -> LDS (lane group g writes head g) -> A operand ----
+        // ---- p and alpha -> LDS (lane group g writes head g) -> A operand ----
         if (g < HPW) {
             float f0 = MfmaTile<F>::kPScale, f1 = MfmaTile<F>::kPScale;
             if constexpr (F != KvFormat::F16) {
@@ -617,18 +602,34 @@ void decode_attention_mfma_kernel(AttnParams p) {
             }
             // x - fp16(x) is exact in fp32; rounding it to fp16 leaves a
             // relative error of 2^-11 of a term that is itself <= 2^-11 x.
-            const float x0 = pr[0][g] * f0, x1 = pr[1][g] * f1;
+            const float x0 = pr0 * f0, x1 = pr1 * f1;
             const uint16_t h0 = f2h_bits(x0), h1 = f2h_bits(x1);
             s_p[wave][0][g][c] = h0;
             s_p[wave][0][g][16 + c] = h1;
             s_p[wave][1][g][c] = f2h_bits(x0 - h2f(h0));
             s_p[wave][1][g][16 + c] = f2h_bits(x1 - h2f(h1));
+            if (c == 0) s_alpha[wave][g] = alpha;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const f16x8 pa = as_f16x8(load16(&s_p[wave][0][c % HPW][8 * g]));
         const f16x8 pl = as_f16x8(load16(&s_p[wave][1][c % HPW][8 * g]));
+        if (rescale) {
+            // PV row 4g + i is head i % HPW (PV's A row m = head m % HPW).
+            const f32x4 al = *reinterpret_cast<const f32x4*>(&s_alpha[wave][0]);
+            float a4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a4[i] = al[i % HPW];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[j][i] *= a4[i];
+            if constexpr (F != KvFormat::F16) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sum_p[i] *= a4[i];
+            }
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
 
@@ -685,9 +686,8 @@ void decode_attention_mfma_kernel(AttnParams p) {
         }
     }
 
-    // ---- merge the 4 wave states through LDS ----
-#pragma unroll
-    for (int i = 0; i < 4; ++i) l[i] = row16_sum(l[i]);
+    // ---- merge the wave states through LDS ----
+    const float l_tot = row16_sum(l_run);   // lane group g: head g's denominator
 
     __shared__ float s_o[NW][HPW][kHeadDim];
     __shared__ float s_m[NW][HPW];
@@ -707,12 +707,9 @@ void decode_attention_mfma_kernel(AttnParams p) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) s_o[wave][i][8 * c + j] = o[j][i] * kInvP;
     }
-    if (lane == 0) {
-#pragma unroll
-        for (int i = 0; i < HPW; ++i) {
-            s_m[wave][i] = m[i];
-            s_l[wave][i] = l[i];
-        }
+    if (c == 0 && g < HPW) {
+        s_m[wave][g] = m_run;
+        s_l[wave][g] = l_tot;
     }
     __syncthreads();
     finish_split<NW, HPW, NW * kWave>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
