@@ -27,7 +27,8 @@ un-expanded [B, Hkv, S, D]. This module plugs into that registry:
   fp16 tokens of the open group, kv_int4_cache.py:225-245); decode sees the
   packed buffers.
 * ``QuantizedLinear`` / ``patch_model_w4a16``: integration/w4a16_patch.py:56-174
-  (W4A16 projections; the GEMM below 256 rows, dequantise + matmul above),
+  (W4A16 projections; the GEMM below the measured crossover, 448-768 rows,
+  dequantise + matmul from there),
   with the weights quantised on the GPU (quantize_pack_weights_int4, the
   same bits as the reference's torch quantiser).
 * ``fused_ops()``: the fused RMSNorm / SwiGLU / RoPE patches of
@@ -261,12 +262,19 @@ def _unpack_int4(p: torch.Tensor) -> torch.Tensor:
 _TARGET_LINEAR_NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "up_proj", "gate_proj", "down_proj")
 
 
+def dequant_path_threshold(N: int) -> int:
+    """Rows from which dequantise + matmul (hipBLASLt) beats w4a16_gemm on
+    MI355X, measured at the Llama-3-8B shapes: ~768 rows for N = 4096 (K =
+    4096 or 14336), ~448 for N = 14336. The reference switches at 256
+    (integration/w4a16_patch.py:89), where w4a16_gemm is 1.5-2.2x faster."""
+    return 768 if N <= 8192 else 448
+
+
 class QuantizedLinear(nn.Module):
     """W4A16 replacement for nn.Linear(bias=False) (integration/w4a16_patch.py:56-141):
     packed INT4 weights [K/8, N] int32 and fp16 scales [K/g, N]; forward runs
-    w4a16_gemm below 256 rows and dequantise + matmul above."""
-
-    DEQUANT_PATH_M_THRESHOLD = 256
+    w4a16_gemm below dequant_path_threshold(N) rows and dequantise + matmul
+    from there."""
 
     def __init__(self, weight_fp16: torch.Tensor, group_size: int = 128) -> None:
         super().__init__()
@@ -282,7 +290,7 @@ class QuantizedLinear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
         x2 = x.reshape(-1, self.in_features).contiguous()
-        if x2.shape[0] < self.DEQUANT_PATH_M_THRESHOLD:
+        if x2.shape[0] < dequant_path_threshold(self.out_features):
             out = w4a16_gemm(x2, self.weight_packed, self.scale, self.group_size)
         else:
             out = torch.matmul(x2, w4a16_dequantize(self.weight_packed, self.scale, self.group_size))
