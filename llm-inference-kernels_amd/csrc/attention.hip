@@ -19,9 +19,10 @@
 //
 // Main kernel (decode_attention_mfma_kernel): each wave walks its own
 // contiguous token range in 32-token tiles on v_mfma_f32_16x16x32_f16:
-//   QK : A = q (16 rows, row m holds head m % HPW), B = 16 tokens' keys
-//        (lane = token, 8 consecutive channels per lane group) -> every lane
-//        gets the scores of its token for all heads; no lane reductions.
+//   QK : A = q (16 rows, row m holds head (m / 4) % HPW), B = 16 tokens'
+//        keys (lane = token, 8 consecutive channels per lane group) -> lane
+//        group g gets head g % HPW's score of its token and runs that head's
+//        online softmax; no cross-group reductions.
 //   PV : A = p as an fp16 hi + lo pair (two MFMAs per B operand, through a
 //        512-byte per-wave LDS slot; fp16 p alone would cost ~2^-12 |v| of
 //        accuracy under a peaked softmax), B = values:
@@ -31,7 +32,9 @@
 //   INT8/INT4 codes are converted to fp16 exactly in registers; the INT8
 //   per-token K scale multiplies the score, the per-token V scale folds into
 //   p, the INT4 per-channel K scale folds into q per group (q*s split into an
-//   fp16 hi + lo pair so the product keeps fp32 precision).
+//   fp16 hi + lo pair in alternate rows of QK's A operand, so the product
+//   keeps fp32 precision at one MFMA per k-step; INT4's PV likewise carries
+//   both P planes in one MFMA, in alternate lane groups' rows).
 // Fallback kernel (decode_attention_valu_kernel): fp32 VALU with 16-lane
 // DPP reductions; used for INT4 group sizes that are not multiples of 32.
 //
@@ -460,8 +463,10 @@ void decode_attention_mfma_kernel(AttnParams p) {
     // group runs the online softmax of one head (PV keeps row m = head m % HPW).
     const uint16_t* qrow = p.q + ((long)b * p.n_heads + head0 + ((c >> 2) % HPW)) * kHeadDim;
 
-    // Q as the A operand (4 k-steps); for INT4 the hi/lo pair of q * k_scale.
-    f16x8 qa[4], qlo[4];
+    // Q as the A operand (4 k-steps). INT4: q * k_scale as an fp16 hi + lo
+    // pair, hi in the even and lo in the odd rows of each lane group's four,
+    // so that one MFMA per k-step yields both (score = row 4g + row 4g + 1).
+    f16x8 qa[4];
     f16x8 qp[4];    // INT4 only: q of channels 32g + 8ks + i4_perm(e), the K operand's order
     if constexpr (F == KvFormat::F16) {
 #pragma unroll
@@ -489,6 +494,12 @@ void decode_attention_mfma_kernel(AttnParams p) {
 
     // P as an fp16 hi + lo pair (plane 0: fp16(x), plane 1: fp16(x - hi)),
     // so that the PV products carry p to ~2^-22 instead of fp16's 2^-12.
+    // fp16 / INT8: two MFMAs per B operand, one per plane. INT4 (kPlaneRows):
+    // PV's A row m holds plane (m / 4) & 1 of head m % HPW, so lane groups 0
+    // and 2 accumulate the hi products and 1 and 3 the lo products in one
+    // MFMA, and the two halves are added once at the end (measured: faster
+    // for INT4, whose QK already carries a hi/lo pair; not for fp16 / INT8).
+    constexpr bool kPlaneRows = (F == KvFormat::I4);
     __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][2][4][kTile];
     // Each head's rescale factor of the tile, for the PV accumulators, which
     // hold all heads in every lane.
@@ -562,8 +573,8 @@ void decode_attention_mfma_kernel(AttnParams p) {
                 for (int ks = 0; ks < 4; ++ks) {
                     const f16x8 sc = as_f16x8(i4_pair_order(tile.ksc[ks]));
                     const f16x8 hi = qp[ks] * sc;
-                    qa[ks] = hi;
-                    qlo[ks] = __builtin_elementwise_fma(qp[ks], sc, -hi);
+                    const f16x8 lo = __builtin_elementwise_fma(qp[ks], sc, -hi);
+                    qa[ks] = (c & 1) ? lo : hi;
                 }
             }
         }
@@ -574,12 +585,12 @@ void decode_attention_mfma_kernel(AttnParams p) {
             for (int ks = 0; ks < 4; ++ks) {
                 const f16x8 kb = tile.kop(x, blk, ks);
                 acc = mfma16x16x32(qa[ks], kb, acc);
-                if constexpr (F == KvFormat::I4) acc = mfma16x16x32(qlo[ks], kb, acc);
             }
             const bool valid = (t0 + 16 * blk + c) < w1;
             float sc = p.scale_log2;
             if constexpr (F == KvFormat::I8) sc *= h2f(tile.ks[blk]);
-            s[blk] = valid ? acc[0] * sc : -INFINITY;
+            const float dot = (F == KvFormat::I4) ? acc[0] + acc[1] : acc[0];
+            s[blk] = valid ? dot * sc : -INFINITY;
         }
 
         // ---- online softmax of lane group g's head over the 32 tokens ----
@@ -613,8 +624,8 @@ void decode_attention_mfma_kernel(AttnParams p) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const f16x8 pa = as_f16x8(load16(&s_p[wave][0][c % HPW][8 * g]));
-        const f16x8 pl = as_f16x8(load16(&s_p[wave][1][c % HPW][8 * g]));
+        const f16x8 pa = as_f16x8(load16(&s_p[wave][kPlaneRows ? (c >> 2) & 1 : 0][c % HPW][8 * g]));
+        const f16x8 pl = kPlaneRows ? pa : as_f16x8(load16(&s_p[wave][1][c % HPW][8 * g]));
         if (rescale) {
             // PV row 4g + i is head i % HPW (PV's A row m = head m % HPW).
             const f32x4 al = *reinterpret_cast<const f32x4*>(&s_alpha[wave][0]);
@@ -638,11 +649,11 @@ void decode_attention_mfma_kernel(AttnParams p) {
         for (int j = 0; j < 8; ++j) {
             const f16x8 vb = tile.vop(x, j);
             o[j] = mfma16x16x32(pa, vb, o[j]);
-            o[j] = mfma16x16x32(pl, vb, o[j]);
+            if constexpr (!kPlaneRows) o[j] = mfma16x16x32(pl, vb, o[j]);
         }
         if constexpr (F != KvFormat::F16) {
             sum_p = mfma16x16x32(pa, ones, sum_p);
-            sum_p = mfma16x16x32(pl, ones, sum_p);
+            if constexpr (!kPlaneRows) sum_p = mfma16x16x32(pl, ones, sum_p);
         }
     };
 
@@ -694,6 +705,14 @@ void decode_attention_mfma_kernel(AttnParams p) {
     __shared__ float s_l[NW][HPW];
     __shared__ uint32_t s_last;
     constexpr float kInvP = 1.0f / MfmaTile<F>::kPScale;
+    if constexpr (kPlaneRows) {   // hi + lo planes: lane group g's PV rows plus lane group g ^ 1's
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[j][i] += __shfl_xor(o[j][i], 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum_p[i] += __shfl_xor(sum_p[i], 16);
+    }
     if constexpr (F != KvFormat::F16) {
 #pragma unroll
         for (int j = 0; j < 8; ++j)

@@ -17,6 +17,7 @@ constexpr int kWave = 64;
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -173,6 +174,16 @@ __device__ __forceinline__ float publish_load(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void publish_wait() { __builtin_amdgcn_s_waitcnt(0); }
+// 16-byte forms through a buffer resource: cache-policy bit 4 of the buffer
+// intrinsics is `sc1`, the same access the relaxed agent-scope atomics above
+// lower to, four floats per instruction.
+constexpr int kPublishAux = 16;
+__device__ __forceinline__ void publish_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, 0, kPublishAux);
+}
+__device__ __forceinline__ u32x4 publish_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, kPublishAux);
+}
 // Returns true in exactly one workgroup: the last of `n` to arrive.
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t n) {
     return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1;

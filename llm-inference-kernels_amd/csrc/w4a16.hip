@@ -41,6 +41,7 @@ struct GemmParams {
     int nw;              // streaming GEMV: waves per workgroup
     int wave_steps;      // streaming GEMV / 32x32 GEMM: 32-K steps per wave
     int m_tiles_;        // 32x32 GEMM: row tiles
+    int vec_out;         // 32x32 GEMM: out is 16-byte aligned (vector stores)
 };
 
 // Eight int4 codes of one word -> four fp16 pairs, exact. Pair j holds the
@@ -112,6 +113,23 @@ __device__ __forceinline__ void store_out(const GemmParams& p, int m, int n, flo
         static_cast<float*>(p.out)[(long)m * p.N + n] = v;
     } else {
         static_cast<uint16_t*>(p.out)[(long)m * p.N + n] = f2h_bits(v);
+    }
+}
+
+// 4 consecutive outputs of row m from column n (a multiple of 4): one 16- /
+// 8-byte store when the output allows it (vec_out: base 16-byte aligned),
+// else one store per value.
+__device__ __forceinline__ void store_out4(const GemmParams& p, int m, int n, const f32x4 v) {
+    const long base = (long)m * p.N + n;
+    if (!p.vec_out) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) store_out(p, m, n + e, v[e]);
+    } else if (p.f32_out) {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + base) = v;
+    } else {
+        const uint32_t lo = (uint32_t)f2h_bits(v[0]) | ((uint32_t)f2h_bits(v[1]) << 16);
+        const uint32_t hi = (uint32_t)f2h_bits(v[2]) | ((uint32_t)f2h_bits(v[3]) << 16);
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + base) = u32x2{lo, hi};
     }
 }
 
@@ -1191,11 +1209,12 @@ __global__ __launch_bounds__(kMmaThreads) void w4a16_gemm_mfma_kernel(GemmParams
                 v[u][o] = publish_load(&p.part[(sp * p.M + m) * p.N + n]);
             }
         }
+        // Padding slots add +0.0f (exact: tot is never -0); unconditional adds
+        // keep both splits' loads ahead of the first use.
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int o = 0; o < NO; ++o)
-                if (s0 + u < p.splits) tot[o] += v[u][o];
+            for (int o = 0; o < NO; ++o) tot[o] += (s0 + u < p.splits) ? v[u][o] : 0.0f;
     }
 #pragma unroll
     for (int o = 0; o < NO; ++o) {
@@ -1459,36 +1478,50 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
         __syncthreads();
     }
 
-    // C layout of v_mfma_f32_32x32x16: value r of lane l is row
-    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 of the 32 x 32 block.
-    auto out_row = [&](int rb, int r) { return m0 + 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3); };
-    if (p.splits == 1) {
-        if (kg == 0) {
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = out_row(rb, r);
-                    if (m < p.M) {
-                        store_out(p, m, n0 + 2 * c, acc[rb][0][r]);
-                        store_out(p, m, n0 + 2 * c + 1, acc[rb][1][r]);
-                    }
-                }
-        }
-        return;
-    }
+    // The workgroup's tile (held by the kg == 0 waves) goes through LDS to
+    // row-major order; thread t then owns columns 4 (t % 32) .. + 3 of rows
+    // t / 32 + 16 i (i < 4), so that every 16-byte access instruction covers
+    // whole rows (32 lanes x 16 bytes): the split partials, their combine and
+    // the output. C layout of v_mfma_f32_32x32x16: value r of lane l is row
+    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 of the block.
+    constexpr int kTRow = 132;   // floats per LDS row (128 + 4 of padding)
+    float* s_t = reinterpret_cast<float*>(&s_a[0][0][0][0]);   // [TM][kTRow]
     if (kg == 0) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = out_row(rb, r);
-                if (m < p.M) {
-                    float* dst = &p.part[((long)split * p.M + m) * p.N + n0 + 2 * c];
-                    publish_store(dst, acc[rb][0][r]);
-                    publish_store(dst + 1, acc[rb][1][r]);
-                }
+                const int row = 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3);
+                *reinterpret_cast<f32x2*>(&s_t[row * kTRow + 64 * ch + 2 * c]) =
+                    f32x2{acc[rb][0][r], acc[rb][1][r]};
             }
+    }
+    __syncthreads();
+    const int tcol = 4 * (threadIdx.x & 31);
+    const int nt0 = tile * 128;
+    f32x4 v[4];
+    int mi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = (threadIdx.x >> 5) + 16 * i;
+        mi[i] = m0 + row;
+        v[i] = *reinterpret_cast<const f32x4*>(&s_t[row * kTRow + tcol]);
+    }
+    if (p.splits == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (mi[i] < p.M) store_out4(p, mi[i], nt0 + tcol, v[i]);
+        return;
+    }
+    const uint32_t slab = (uint32_t)p.M * p.N * 4u;   // bytes per split (plan: < 2 GiB)
+    uint32_t off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) off[i] = ((uint32_t)min(mi[i], p.M - 1) * p.N + nt0 + tcol) * 4u;
+    {
+        const __amdgpu_buffer_rsrc_t rp = make_buffer_rsrc(p.part + (long)split * p.M * p.N, slab);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (mi[i] < p.M) publish_store16(rp, off[i], __builtin_bit_cast(u32x4, v[i]));
     }
     publish_wait();
     __syncthreads();
@@ -1496,41 +1529,37 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
     if (threadIdx.x == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
-    // Last split of the tile: each thread adds the splits of its kPer
-    // outputs in split order, with the loads of two splits for all of them
-    // issued together (a few memory round trips per tile, not one per output).
-    constexpr int kPer = TM * 128 / kG32Threads;
-    const long mn = (long)p.M * p.N;
-    const int nt0 = tile * 128;
-    float tot[kPer];
-    long idx[kPer];
+    // Last split of the tile: the partials are added in split order, with the
+    // loads of two splits issued together. The padding slot adds +0.0f, an
+    // exact no-op (the sum starts at +0 and is never -0); the unconditional
+    // add keeps both batches' loads ahead of the first use.
+    f32x4 tot[4];
 #pragma unroll
-    for (int o = 0; o < kPer; ++o) {
-        const int e = threadIdx.x + o * kG32Threads;
-        const int m = min(m0 + e / 128, p.M - 1);
-        idx[o] = (long)m * p.N + nt0 + e % 128;
-        tot[o] = 0.0f;
-    }
+    for (int i = 0; i < 4; ++i) tot[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < p.splits; s0 += 2) {
-        float x[2][kPer];
+        u32x4 x[2][4];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const long base = (long)min(s0 + u, p.splits - 1) * mn;
+            const int sp = min(s0 + u, p.splits - 1);
+            const __amdgpu_buffer_rsrc_t rp = make_buffer_rsrc(p.part + (long)sp * p.M * p.N, slab);
 #pragma unroll
-            for (int o = 0; o < kPer; ++o) x[u][o] = publish_load(p.part + base + idx[o]);
+            for (int i = 0; i < 4; ++i) x[u][i] = publish_load16(rp, off[i]);
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u) {
+            const bool live = s0 + u < p.splits;
 #pragma unroll
-            for (int o = 0; o < kPer; ++o)
-                if (s0 + u < p.splits) tot[o] += x[u][o];
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t b = x[u][i][e];
+                    tot[i][e] += live ? __uint_as_float(b) : 0.0f;
+                }
+        }
     }
 #pragma unroll
-    for (int o = 0; o < kPer; ++o) {
-        const int e = threadIdx.x + o * kG32Threads;
-        const int m = m0 + e / 128;
-        if (m < p.M) store_out(p, m, nt0 + e % 128, tot[o]);
-    }
+    for (int i = 0; i < 4; ++i)
+        if (mi[i] < p.M) store_out4(p, mi[i], nt0 + tcol, tot[i]);
     if (threadIdx.x == 0) p.counters[counter] = 0u;
 }
 
@@ -1832,7 +1861,7 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
         return pl;
     }
     if (M > 16 && N % 128 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31) &&
-        (long)M * K * 2 < (1L << 31)) {
+        (long)M * K * 2 < (1L << 31) && (long)M * N * 4 < (1L << 31)) {
         // 32x32x16 matrix-core GEMM: tiles of 64 rows by 128 columns, 8 waves
         // = 2 column halves x 4 K ranges of whole scale groups; K splits
         // until the tiles fill the CUs once (no second round).
@@ -1962,6 +1991,7 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
         else launch_gemv16_cb<2, false>(p, grid, stream);
     } else if (pl.kind == 6) {
         p.m_tiles_ = pl.m_tiles;
+        p.vec_out = (reinterpret_cast<uintptr_t>(out) % 16 == 0) ? 1 : 0;
         const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kG32Threads);
         hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel, grid, blk, 0, stream, p);
     } else if (pl.kind == 3) {
