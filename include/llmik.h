@@ -233,7 +233,10 @@ LLMIK_API llmik_status llmik_kivi_append_token_int4(
  *   act           [M, K] fp16
  *   weight_packed [K/8, N] uint32 (int4 along K)
  *   scale         [K/group_size, N] fp16
- * group_size must be a positive multiple of 8 dividing K.
+ * group_size must be a positive multiple of 8 dividing K. act and
+ * weight_packed need 16-byte, scale 8-byte and out 4-byte alignment; a
+ * 16-byte aligned out lets the M > 16 matrix-core GEMM store 8 / 16 bytes
+ * at a time (otherwise it stores one value at a time).
  */
 LLMIK_API size_t llmik_w4a16_workspace_size(int M, int N, int K, int group_size);
 

@@ -297,7 +297,8 @@ int check_gemm(const void* act, const void* w, const void* scale, const void* ou
     if (K % group_size != 0) return invalid("K must equal n_groups * group_size");
     if ((long)M * N > 0 && K > 0 && (!act || !w || !scale || !out)) return invalid("null pointer");
     if (!aligned(act, 16) || !aligned(w, 16) || !aligned(scale, 8) || !aligned(out, 4))
-        return set_error(LLMIK_ERR_ALIGNMENT, "act/weight must be 16-byte aligned");
+        return set_error(LLMIK_ERR_ALIGNMENT,
+                         "act/weight must be 16-byte, scale 8-byte and out 4-byte aligned");
     return LLMIK_OK;
 }
 }  // namespace

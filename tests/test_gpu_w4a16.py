@@ -88,6 +88,36 @@ def test_odd_shapes(llmik, cuda, M, K, N, gs):
     _check(llmik, cuda, M, K, N, gs, seed=M * 7 + K)
 
 
+@pytest.mark.parametrize("M,K,N,f32", [(128, 4096, 4096, False), (128, 4096, 4096, True),
+                                      (300, 128, 256, False)])
+def test_unaligned_output_pointer(llmik, cuda, M, K, N, f32):
+    """The 32x32 GEMM stores 8 / 16 bytes at a time only when the output is
+    16-byte aligned. An output 4 bytes off (the C ABI's minimum alignment for
+    out; a caller's offset view) takes the per-value stores: same bits as the
+    aligned output, nothing written outside it. (128, 4096, 4096) splits K;
+    (300, 128, 256) does not."""
+    from llmik_cuda._lib import lib
+    q, s, packed = _weights(K, N, 128, 5)
+    a = _dev(randn((M, K), 6).astype(np.float16), cuda)
+    w, sc = _dev(packed, cuda), _dev(s, cuda)
+    dt = torch.float32 if f32 else torch.float16
+    ref = (llmik.w4a16_gemm_f32out if f32 else llmik.w4a16_gemm)(a, w, sc, 128)
+    buf = torch.full((M * N + 8,), float("nan"), dtype=dt, device=cuda)
+    need = lib.llmik_w4a16_workspace_size(M, N, K, 128)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=cuda)
+    fn = lib.llmik_w4a16_gemm_f32out if f32 else lib.llmik_w4a16_gemm
+    torch.cuda.synchronize()
+    off = 4 // buf.element_size()
+    st = fn(a.data_ptr(), w.data_ptr(), sc.data_ptr(), buf.data_ptr() + 4,
+            M, N, K, 128, ws.data_ptr() if need else None, need,
+            torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.llmik_last_error()
+    torch.cuda.synchronize()
+    bits = torch.int32 if f32 else torch.int16
+    assert torch.equal(buf[off:off + M * N].view(bits), ref.reshape(-1).view(bits))
+    assert bool(torch.isnan(buf[:off]).all()) and bool(torch.isnan(buf[off + M * N:]).all())
+
+
 def test_deterministic(llmik, cuda):
     q, s, packed = _weights(4096, 4096, 128, 1)
     a = _dev(randn((16, 4096), 2).astype(np.float16), cuda)
