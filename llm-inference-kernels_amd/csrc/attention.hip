@@ -17,8 +17,8 @@
 //     a (batch, kv_head, head_chunk) merges all splits in split order and
 //     writes fp16 out, so a call is one launch and results are deterministic.
 //
-// Main kernel (decode_attention_mfma_kernel): each wave walks its own
-// contiguous token range in 32-token tiles on v_mfma_f32_16x16x32_f16:
+// Main kernel (decode_attention_mfma_kernel): each wave walks its tiles of
+// 32 tokens on v_mfma_f32_16x16x32_f16:
 //   QK : A = q (16 rows, row m holds head (m / 4) % HPW), B = 16 tokens'
 //        keys (lane = token, 8 consecutive channels per lane group) -> lane
 //        group g gets head g % HPW's score of its token and runs that head's
@@ -439,10 +439,11 @@ struct MfmaTile<KvFormat::I4> {
     }
 };
 
-// NW waves per workgroup. fp16 / INT8: the waves take the split's 32-token
-// tiles round robin, so the workgroup streams one contiguous region and its
-// waves finish within a tile of each other. INT4: each wave takes a
-// contiguous quarter / eighth of the split, so its K-scale group changes
+// NW waves per workgroup. fp16: split s takes the sequence's 32-token tiles
+// s, s + n_splits, ... and its waves take those round robin. INT8: the waves
+// take the split's contiguous range of tiles round robin. Either way a
+// workgroup's waves finish within a tile of each other. INT4: each wave takes
+// a contiguous quarter / eighth of the split, so its K-scale group changes
 // only every group_size tokens.
 template <KvFormat F, int HPW, int NW>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
@@ -509,8 +510,17 @@ void decode_attention_mfma_kernel(AttnParams p) {
     const int t_end = min(t_begin + p.chunk, p.seqlen);
     constexpr bool kInterleave = (F != KvFormat::I4);
     constexpr int kWaveStride = kInterleave ? NW * kTile : kTile;
+    // fp16: split s takes tiles s, s + n_splits, s + 2 n_splits, ... of the
+    // whole sequence and its waves every NW-th of those, so each workgroup's
+    // reads spread over its KV head's whole K and V instead of one
+    // contiguous quarter (measured faster at B=1, S >= 16384 and B=64; INT8
+    // keeps contiguous split ranges, where the same change was slower).
+    constexpr bool kSplitTiles = (F == KvFormat::F16);
     int w0, w1;
-    if constexpr (kInterleave) {
+    if constexpr (kSplitTiles) {
+        w0 = (split + p.n_splits * wave) * kTile;
+        w1 = p.seqlen;
+    } else if constexpr (kInterleave) {
         w0 = t_begin + wave * kTile;
         w1 = t_end;
     } else {
@@ -668,7 +678,8 @@ void decode_attention_mfma_kernel(AttnParams p) {
         // One 16 / 8 KiB fp16 / INT8 tile per wave in flight already keeps
         // 32 / 16 MiB of loads queued chip-wide; a second one only lengthens
         // the queue (measured slower for both).
-        for (int t0 = w0; t0 < w1; t0 += kWaveStride) {
+        const int stride = kSplitTiles ? p.n_splits * NW * kTile : kWaveStride;
+        for (int t0 = w0; t0 < w1; t0 += stride) {
             MfmaTile<F> tile;
             load_tile(tile, t0);
             __builtin_amdgcn_sched_barrier(0);
