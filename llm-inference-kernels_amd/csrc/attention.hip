@@ -291,12 +291,16 @@ struct MfmaTile<KvFormat::F16> {
     // 8g + e, channels 8c.
     __device__ __forceinline__ void load(const TileCtx& x, int t0) {
         const uint32_t so = (uint32_t)t0 * kRow;
+        // Each K instruction reads 64 bytes of every row (half a 128-byte
+        // line; the next k-step's instruction reads the rest), so K is loaded
+        // without the non-temporal hint and the line waits in L2 for its
+        // second half. V instructions read whole rows and keep the hint.
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
                 k[blk][ks] = __builtin_amdgcn_raw_buffer_load_b128(
-                    x.rk, (int)x.koff, (int)(so + 16 * kRow * blk + 64 * ks), 2);
+                    x.rk, (int)x.koff, (int)(so + 16 * kRow * blk + 64 * ks), 0);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             v[e] = __builtin_amdgcn_raw_buffer_load_b128(x.rv, (int)x.voff, (int)(so + kRow * e), 2);
@@ -330,9 +334,9 @@ struct MfmaTile<KvFormat::I8> {
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < 2; ++u)   // half rows: no non-temporal hint (see the fp16 tile)
                 k[blk][u] = __builtin_amdgcn_raw_buffer_load_b128(
-                    x.rk, (int)x.koff, (int)(so + 16 * kRow * blk + 64 * u), 2);
+                    x.rk, (int)x.koff, (int)(so + 16 * kRow * blk + 64 * u), 0);
             ks[blk] = __builtin_amdgcn_raw_buffer_load_b16(x.rks, (int)x.soff, (int)(2 * t0 + 32 * blk), 0);
             vs[blk] = __builtin_amdgcn_raw_buffer_load_b16(x.rvs, (int)x.soff, (int)(2 * t0 + 32 * blk), 0);
         }
