@@ -443,9 +443,8 @@ struct MfmaTile<KvFormat::I4> {
     }
 };
 
-// NW waves per workgroup. fp16: split s takes the sequence's 32-token tiles
-// s, s + n_splits, ... and its waves take those round robin. INT8: the waves
-// take the split's contiguous range of tiles round robin. Either way a
+// NW waves per workgroup. fp16 / INT8: split s takes the sequence's 32-token
+// tiles s, s + n_splits, ... and its waves take those round robin, so a
 // workgroup's waves finish within a tile of each other. INT4: each wave takes
 // a contiguous quarter / eighth of the split, so its K-scale group changes
 // only every group_size tokens.
@@ -513,20 +512,17 @@ void decode_attention_mfma_kernel(AttnParams p) {
     const int t_begin = split * p.chunk;
     const int t_end = min(t_begin + p.chunk, p.seqlen);
     constexpr bool kInterleave = (F != KvFormat::I4);
-    constexpr int kWaveStride = kInterleave ? NW * kTile : kTile;
-    // fp16: split s takes tiles s, s + n_splits, s + 2 n_splits, ... of the
-    // whole sequence and its waves every NW-th of those, so each workgroup's
-    // reads spread over its KV head's whole K and V instead of one
-    // contiguous quarter (measured faster at B=1, S >= 16384 and B=64; INT8
-    // keeps contiguous split ranges, where the same change was slower).
-    constexpr bool kSplitTiles = (F == KvFormat::F16);
+    constexpr int kWaveStride = kTile;   // INT4: the wave walks its range tile by tile
+    // fp16 / INT8: split s takes tiles s, s + n_splits, s + 2 n_splits, ...
+    // of the whole sequence and its waves every NW-th of those, so each
+    // workgroup's reads spread over its KV head's whole K and V instead of
+    // one contiguous quarter (measured faster at A8, B=1, S >= 16384 and
+    // B=64; neutral at A16).
+    constexpr bool kSplitTiles = kInterleave;
     int w0, w1;
     if constexpr (kSplitTiles) {
         w0 = (split + p.n_splits * wave) * kTile;
         w1 = p.seqlen;
-    } else if constexpr (kInterleave) {
-        w0 = t_begin + wave * kTile;
-        w1 = t_end;
     } else {
         const int per_wave = p.chunk / NW;   // multiple of kTile
         w0 = min(t_begin + wave * per_wave, t_end);
@@ -682,8 +678,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
         // One 16 / 8 KiB fp16 / INT8 tile per wave in flight already keeps
         // 32 / 16 MiB of loads queued chip-wide; a second one only lengthens
         // the queue (measured slower for both).
-        const int stride = kSplitTiles ? p.n_splits * NW * kTile : kWaveStride;
-        for (int t0 = w0; t0 < w1; t0 += stride) {
+        for (int t0 = w0; t0 < w1; t0 += p.n_splits * NW * kTile) {
             MfmaTile<F> tile;
             load_tile(tile, t0);
             __builtin_amdgcn_sched_barrier(0);
