@@ -26,9 +26,11 @@
 //   PV : A = p as an fp16 hi + lo pair (two MFMAs per B operand, through a
 //        512-byte per-wave LDS slot; fp16 p alone would cost ~2^-12 |v| of
 //        accuracy under a peaked softmax), B = values:
-//        lane (g, c) loads the channels 8c..8c+7 of tokens 8g..8g+7 (full
-//        cache rows per load instruction) and one v_perm_b32 per dword turns
-//        them into the B operand of MFMA j, which owns channels 8c + j.
+//        lane (g, c) loads the channels 8c..8c+7 of the tokens in k-slots
+//        8g..8g+7 (tokens 8g + e; INT4, whose rows are 64 bytes: tokens
+//        4e + g, so that each load instruction reads whole lines) and one
+//        v_perm_b32 per dword turns them into the B operand of MFMA j, which
+//        owns channels 8c + j.
 //   INT8/INT4 codes are converted to fp16 exactly in registers; the INT8
 //   per-token K scale multiplies the score, the per-token V scale folds into
 //   p, the INT4 per-channel K scale folds into q per group (q*s split into an
@@ -402,7 +404,7 @@ struct MfmaTile<KvFormat::I4> {
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            v[e] = __builtin_amdgcn_raw_buffer_load_b32(x.rv, (int)x.voff, (int)(so + kRow * e), 2);
+            v[e] = __builtin_amdgcn_raw_buffer_load_b32(x.rv, (int)x.voff, (int)(so + 4 * kRow * e), 2);
     }
     // Eight codes of a dword -> fp16 pairs (n0,n4), (n1,n5), (n2,n6), (n3,n7), exact.
     // (w ^ 0x88888888) & m | 0x6400 6400 == (w & m) ^ x.x_lo / x.x_hi: the
@@ -556,7 +558,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
             x.voff = 8u * g * kRow + 8u * c;
         } else {
             x.koff = (uint32_t)c * kRow + 16u * g;
-            x.voff = 8u * g * kRow + 4u * c;
+            x.voff = (uint32_t)g * kRow + 4u * c;   // token 4e + g in instruction e
         }
         x.soff = 2u * c;
         x.kgoff = 64u * g;
@@ -625,10 +627,14 @@ void decode_attention_mfma_kernel(AttnParams p) {
             // relative error of 2^-11 of a term that is itself <= 2^-11 x.
             const float x0 = pr0 * f0, x1 = pr1 * f1;
             const uint16_t h0 = f2h_bits(x0), h1 = f2h_bits(x1);
-            s_p[wave][0][g][c] = h0;
-            s_p[wave][0][g][16 + c] = h1;
-            s_p[wave][1][g][c] = f2h_bits(x0 - h2f(h0));
-            s_p[wave][1][g][16 + c] = f2h_bits(x1 - h2f(h1));
+            // INT4: PV's k-slot 8 kq + e holds token 4 e + kq (each V load
+            // instruction then reads four adjacent 64-byte rows, whole lines).
+            const int sl0 = (F == KvFormat::I4) ? 8 * (c & 3) + (c >> 2) : c;
+            const int sl1 = (F == KvFormat::I4) ? sl0 + 4 : 16 + c;
+            s_p[wave][0][g][sl0] = h0;
+            s_p[wave][0][g][sl1] = h1;
+            s_p[wave][1][g][sl0] = f2h_bits(x0 - h2f(h0));
+            s_p[wave][1][g][sl1] = f2h_bits(x1 - h2f(h1));
             if (c == 0) s_alpha[wave][g] = alpha;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
