@@ -1728,14 +1728,16 @@ __global__ __launch_bounds__(256) void w4a16_dequantize_kernel(const uint32_t* _
 // ---------------------------------------------------------------------------
 
 // Streaming GEMV selection: 1 forces it wherever the shape allows, 0
-// disables it; unset (-1), it serves weights of at least
-// kStreamMinWeightBytes (below that the single-row / 16-row GEMVs with
-// 32-column tiles have less fixed cost per call). A positive split count
+// disables it; unset (-1), it serves packed weights of more than
+// kStreamMinWeightBytes. Measured on MI355X at M = 1, 8 and 16: the
+// single-row / 16-row GEMVs with 32-column tiles are faster at (4096, 4096)
+// (8 MiB) and (14336, 1024); the streaming GEMV from (4096, 4608) (9 MiB)
+// and at (14336, 2048) up (up to 27 % faster at M = 16). A positive split count
 // forces the streaming GEMV's K split count (clamped to what the K extent
 // allows). Both are measurement knobs: read once from LLMIK_W4A16_STREAM /
 // LLMIK_W4A16_STREAM_SPLITS when the library loads, and settable with
 // llmik_w4a16_set_plan_override.
-constexpr long kStreamMinWeightBytes = 16L << 20;
+constexpr long kStreamMinWeightBytes = 8L << 20;
 
 namespace {
 int env_int(const char* name, bool as_flag) {
@@ -1759,7 +1761,7 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     GemmPlan pl{};
     const bool pow2_group = group_size >= 32 && (group_size & (group_size - 1)) == 0;
     const int stream_mode = stream_override();
-    const bool stream_size_ok = (long)K * N / 2 >= kStreamMinWeightBytes;
+    const bool stream_size_ok = (long)K * N / 2 > kStreamMinWeightBytes;
     if (M >= 1 && M <= 16 && N % 64 == 0 && pow2_group && K % 32 == 0 &&
         (long)(K / 8) * N * 4 < (1L << 31) && (long)M * K * 2 < (1L << 31) &&
         (stream_mode == 1 || (stream_mode < 0 && stream_size_ok))) {

@@ -10,7 +10,7 @@ group); M = 1 and 2..16; more tiles than CUs (a second round of
 workgroups); and split counts forced with llmik_w4a16_set_plan_override.
 
 The library serves these shapes with the streaming kernel when the packed
-weights reach 16 MiB; the tests force it (llmik_w4a16_set_plan_override) so that the small
+weights exceed 8 MiB; the tests force it (llmik_w4a16_set_plan_override) so that the small
 shapes take it too. Every packed word is random (every code -8..7 occurs),
 scales are random positive fp16, and the reference is act @ (code * scale)
 accumulated in float64 on the GPU in K chunks. Gate (written here): the
@@ -75,7 +75,7 @@ def _set_plan(stream_mode: int, splits: int) -> None:
 @pytest.fixture(autouse=True)
 def _force_stream(llmik):
     """Route every eligible shape to the streaming kernel (the library
-    otherwise keeps it for weights of 16 MiB and more); restore the planner
+    otherwise keeps it for weights of more than 8 MiB); restore the planner
     afterwards."""
     _set_plan(1, -1)
     yield
