@@ -1778,7 +1778,14 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
         const int need = (int)((steps + want - 1) / want);
         int best_nw = kStreamMaxWaves, best_ws = 0;
         long best_waste = -1;
-        for (int nw = kStreamMaxWaves; nw >= kStreamMaxWaves / 2; --nw) {
+        // Among equally padded choices: the most waves per workgroup when
+        // the workgroups fit the CUs in one round; the fewest (8, two
+        // workgroups per CU at <= 128 VGPRs) when they do not, so that they
+        // all stay resident (N = 28672: M=8 18.5-19.0 -> 17.3-18.0 us,
+        // M=16 21.0-22.3 -> 20.0).
+        const bool two_rounds = (long)tiles * want > device_cu_count();
+        for (int i = 0; i <= kStreamMaxWaves / 2; ++i) {
+            const int nw = two_rounds ? kStreamMaxWaves / 2 + i : kStreamMaxWaves - i;
             int ws = (need + nw - 1) / nw;
             ws = ws <= 2 ? 2 : ws <= 4 ? 4 : (ws + 7) / 8 * 8;
             const long waste = (long)nw * ws - need;
