@@ -973,8 +973,15 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
     const long splits8 = ((long)seqlen + 8 * kTile - 1) / (8 * kTile);
     const bool short_seq = base_wgs * splits8 < target && 2 * splits8 <= 8;
     pl.waves = (base_wgs < target && !short_seq) ? 8 : 4;
+    // Splits that would give each of 8 waves a single 32-token tile run as
+    // 4-wave workgroups at twice the split count (two per CU), as long as the
+    // combine stays at <= 8 partials: B=8, S=1024 11.36-11.40 -> 10.94-11.03
+    // us; with more partials (B=4, S=1024; B=1, S=4096) it was slower.
+    const bool thin = pl.waves == 8 && (long)seqlen * base_wgs <= target * 8 * kTile &&
+                      2 * ((target + base_wgs - 1) / base_wgs) <= 8;
+    if (thin) pl.waves = 4;
     const int step = kTile * pl.waves;
-    long want = (target + base_wgs - 1) / base_wgs;
+    long want = ((thin ? 2 : 1) * target + base_wgs - 1) / base_wgs;
     const long max_useful = (seqlen + step - 1) / step;
     if (want > max_useful) want = max_useful;
     if (want > kMaxAttnSplits) want = kMaxAttnSplits;
