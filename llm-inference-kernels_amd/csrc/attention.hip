@@ -518,8 +518,8 @@ void decode_attention_mfma_kernel(AttnParams p) {
     // fp16 / INT8: split s takes tiles s, s + n_splits, s + 2 n_splits, ...
     // of the whole sequence and its waves every NW-th of those, so each
     // workgroup's reads spread over its KV head's whole K and V instead of
-    // one contiguous quarter (measured faster at A8, B=1, S >= 16384 and
-    // B=64; neutral at A16).
+    // one contiguous quarter (fp16, against contiguous ranges: A16 and B=1
+    // 1-3 % faster, S=16384 and B=64 about 1 % slower; INT8 neutral).
     constexpr bool kSplitTiles = kInterleave;
     int w0, w1;
     if constexpr (kSplitTiles) {

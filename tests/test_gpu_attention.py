@@ -188,6 +188,23 @@ def test_fp16_swept_baseline_configs(llmik, cuda, B, L):
     assert torch.equal(out_p, out[perm])
 
 
+@pytest.mark.parametrize("B,L", [(8, 16385), (32, 600), (64, 4100)])
+def test_fp16_ragged_interleaved_tiles(llmik, cuda, B, L):
+    """Ragged lengths under the interleaved tile order (split s, wave w reads
+    tiles s + n_splits * (w + NW * i)): B=8, S=16385 (4 splits; the one-token
+    last tile falls to split 0, wave 0, its 17th tile), B=32, S=600 (4-wave
+    workgroups, no split, a 24-token last tile) and B=64, S=4100 (a 4-token
+    last tile). Oracle parity on sampled batch rows."""
+    gen = torch.Generator(device=cuda).manual_seed(B * 3 + L)
+    kd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    vd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    q = randn((B, 32, 128), B * 11 + L).astype(np.float16)
+    scale = 1 / math.sqrt(128)
+    out = llmik.decode_attention(_dev(q, cuda), kd, vd, scale)
+    _sampled_rows_parity(out, q, lambda b: kd[b:b + 1].cpu().numpy(),
+                         lambda b: vd[b:b + 1].cpu().numpy(), (0, B // 2, B - 1), scale)
+
+
 def _peaked_inputs(B, L, seed):
     """q heads of a kv group share one direction; three tokens of each (b, kv
     head) have keys along it (scores ~12 against ~N(0,1) for the rest), so
