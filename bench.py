@@ -30,10 +30,13 @@ Method
     after 3 warm-up calls, at the headline shape.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-details] [--no-cpu]
+       python bench.py --floors          (empty-kernel and plain-read floors)
+       python bench.py --pmc-workload X  (the program the counter passes profile)
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -560,6 +563,71 @@ def cpu_details(budget_s: float = 3.0):
     return out
 
 
+# ------------------------------------------------------------------ floors
+
+FLOOR_SIZES = (
+    ("w4a16 (4096, 4096) M=1", w4a16_bytes(1, 4096, 4096)),
+    ("w4a16 (4096, 14336) M=1", w4a16_bytes(1, 4096, 14336)),
+    ("attention A16 K and V", 2 * 8 * 8 * 4096 * 128 * 2),
+    ("1 GiB", 1 << 30),
+)
+FLOOR_GRIDS = (256, 1024, 2048)
+FLOOR_LOADS = (4, 8, 16)
+
+
+def bench_floors(steps: int, warmup: int) -> list:
+    """What one launch costs before it does any work, and what the plainest
+    read of a product kernel's bytes costs (llmik_diag_empty /
+    llmik_diag_read, csrc/diag.hip), timed like every other row: graph
+    replay of `steps` calls over rotating windows of one buffer (>= 768 MiB
+    in all). Each read size runs at every grid in FLOOR_GRIDS (workgroups of
+    8 waves) and every depth in FLOOR_LOADS (16-byte loads per lane in
+    flight); the empty kernel at 256 and 1024 workgroups. Rows are printed
+    in the order their dispatches run: for each, max(warmup, windows) eager
+    calls, then two graph replays of max(steps, windows) calls. A last row
+    per size names the fastest read."""
+    import torch
+    from llmik_cuda._lib import check, lib
+    dev = torch.device("cuda:0")
+    rows = []
+
+    def stream_ptr():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    for nwg in (256, 1024):
+        fn = (lambda n=nwg: check(lib.llmik_diag_empty(n, stream_ptr())))
+        us = time_steps([fn], warmup, steps)
+        rows.append({"name": f"empty kernel, {nwg} x 512 threads", "n_workgroups": nwg,
+                     "calls": max(warmup, 1) + 2 * steps, "us": round(us, 3)})
+        log(rows[-1])
+    for name, nbytes in FLOOR_SIZES:
+        nbytes = (nbytes + 255) // 256 * 256
+        n_sets = n_sets_for(nbytes)
+        buf = torch.randint(0, 256, (n_sets * nbytes,), dtype=torch.uint8, device=dev)
+        size_rows = []
+        for nwg in FLOOR_GRIDS:
+            sink = torch.zeros(nwg * 8, dtype=torch.int32, device=dev)
+            for L in FLOOR_LOADS:
+                fns = [(lambda i=i, n=nwg, sk=sink, L=L:
+                        check(lib.llmik_diag_read(ctypes.c_void_p(buf.data_ptr() + i * nbytes), nbytes,
+                                                  ctypes.c_void_p(sk.data_ptr()), n, L, stream_ptr())))
+                       for i in range(n_sets)]
+                us = time_steps(fns, warmup, steps)
+                size_rows.append({"name": f"read {name}", "bytes": nbytes, "n_workgroups": nwg,
+                                  "loads_per_lane": L, "windows": n_sets,
+                                  "calls": max(warmup, n_sets) + 2 * max(steps, n_sets),
+                                  "us": round(us, 3), "TBps": round(nbytes / us / 1e6, 3)})
+                log(size_rows[-1])
+        best = min(size_rows, key=lambda r: r["us"])
+        rows.extend(size_rows)
+        rows.append({"name": f"fastest read {name}", "bytes": nbytes, "us": best["us"],
+                     "TBps": best["TBps"], "n_workgroups": best["n_workgroups"],
+                     "loads_per_lane": best["loads_per_lane"]})
+        del buf
+        torch.cuda.synchronize()
+    return rows
+
+
 # ------------------------------------------------------------- HBM traffic
 
 PMC_WORKLOADS = ("attn:fp16", "attn:int8", "attn:int4", "attn:int4g32", "attn:int4b64",
@@ -664,6 +732,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list: int8,int4,w4a16,prefill,layer,writers,append,sweep,wquant")
+    ap.add_argument("--floors", action="store_true",
+                    help="time the empty-kernel and plain-read floors (csrc/diag.hip), print one "
+                         "JSON line per row and exit")
     ap.add_argument("--pmc-workload", nargs="?", const="attn:fp16", default=None,
                     choices=PMC_WORKLOADS,
                     help="run a counter-collection program (one kernel family's calls, then "
@@ -681,6 +752,10 @@ def main() -> None:
     log(f"device {torch.cuda.get_device_name(0)}; library {llmik.LIB_PATH}")
     if args.pmc_workload:
         pmc_workload(llmik, args.pmc_workload, args.steps)
+        return
+    if args.floors:
+        for row in bench_floors(args.steps, args.warmup):
+            print(json.dumps(row), flush=True)
         return
 
     only = set(filter(None, args.only.split(",")))

@@ -1,0 +1,87 @@
+// Measurement kernels: the floors that the product kernels' rooflines are
+// read against. Neither has a counterpart in the reference; bench.py's
+// --floors mode and the profile summaries that quote these floors run them.
+//
+// diag_empty_kernel: a launch that does nothing, the per-dispatch cost of a
+// kernel of the same workgroup size.
+//
+// diag_read_kernel<L>: the plainest fast read this library knows how to
+// issue. Each wave reads L KiB contiguous per iteration (L 16-byte buffer
+// loads per lane, all issued before any is used, with the non-temporal
+// hint), waves take L KiB units round robin over the grid, and the loaded
+// words are folded with xor so that the loads cannot be dropped. One 32-bit
+// value per wave is written: the xor of every word the wave read.
+#include "device_common.hpp"
+#include "llmik_internal.hpp"
+
+namespace llmik {
+namespace {
+
+constexpr int kDiagWaves = 8;
+constexpr size_t kDiagMaxBytes = (size_t)3 << 30;   // offsets stay 32-bit
+
+__global__ __launch_bounds__(kDiagWaves * kWave) void diag_empty_kernel() {}
+
+template <int L>
+__global__ __launch_bounds__(kDiagWaves * kWave) void diag_read_kernel(const void* src, uint32_t bytes,
+                                                                         uint32_t* sink) {
+    constexpr uint32_t kUnit = kWave * 16u * L;   // bytes per wave per iteration
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t gw = blockIdx.x * kDiagWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n_waves = gridDim.x * kDiagWaves;
+    // Loads past `bytes` read zeros (buffer bound), which leave the xor unchanged.
+    const __amdgpu_buffer_rsrc_t r = make_buffer_rsrc(src, bytes);
+    const uint32_t n_units = (bytes + kUnit - 1) / kUnit;
+    uint32_t x = 0;
+    for (uint32_t u = gw; u < n_units; u += n_waves) {
+        u32x4 v[L];
+#pragma unroll
+        for (int i = 0; i < L; ++i)
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(lane * 16u),
+                                                         (int)(u * kUnit + (uint32_t)i * 1024u), 2);
+#pragma unroll
+        for (int i = 0; i < L; ++i) x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o);
+    if (lane == 0) sink[gw] = x;
+}
+
+}  // namespace
+}  // namespace llmik
+
+extern "C" {
+
+LLMIK_API llmik_status llmik_diag_empty(int n_workgroups, void* stream) {
+    if (n_workgroups <= 0) return llmik::set_error(LLMIK_ERR_INVALID, "llmik_diag_empty: n_workgroups must be > 0");
+    hipLaunchKernelGGL(llmik::diag_empty_kernel, dim3((unsigned)n_workgroups),
+                       dim3(llmik::kDiagWaves * llmik::kWave), 0, static_cast<hipStream_t>(stream));
+    return llmik::check_launch();
+}
+
+LLMIK_API llmik_status llmik_diag_read(const void* src, size_t bytes, void* sink, int n_workgroups,
+                                       int loads_per_lane, void* stream) {
+    if (n_workgroups <= 0) return llmik::set_error(LLMIK_ERR_INVALID, "llmik_diag_read: n_workgroups must be > 0");
+    if (bytes % 16 != 0 || bytes > llmik::kDiagMaxBytes)
+        return llmik::set_error(LLMIK_ERR_INVALID,
+                                "llmik_diag_read: bytes must be a multiple of 16 and at most 3 GiB");
+    if (loads_per_lane != 4 && loads_per_lane != 8 && loads_per_lane != 16)
+        return llmik::set_error(LLMIK_ERR_INVALID, "llmik_diag_read: loads_per_lane must be 4, 8 or 16");
+    if (src == nullptr || sink == nullptr)
+        return llmik::set_error(LLMIK_ERR_INVALID, "llmik_diag_read: null pointer");
+    if (reinterpret_cast<uintptr_t>(src) % 16 != 0 || reinterpret_cast<uintptr_t>(sink) % 4 != 0)
+        return llmik::set_error(LLMIK_ERR_ALIGNMENT,
+                                "llmik_diag_read: src must be 16-byte and sink 4-byte aligned");
+    const dim3 grid((unsigned)n_workgroups), block(llmik::kDiagWaves * llmik::kWave);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* out = static_cast<uint32_t*>(sink);
+    if (loads_per_lane == 4)
+        hipLaunchKernelGGL(llmik::diag_read_kernel<4>, grid, block, 0, st, src, (uint32_t)bytes, out);
+    else if (loads_per_lane == 8)
+        hipLaunchKernelGGL(llmik::diag_read_kernel<8>, grid, block, 0, st, src, (uint32_t)bytes, out);
+    else
+        hipLaunchKernelGGL(llmik::diag_read_kernel<16>, grid, block, 0, st, src, (uint32_t)bytes, out);
+    return llmik::check_launch();
+}
+
+}  // extern "C"

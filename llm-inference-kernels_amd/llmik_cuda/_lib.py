@@ -58,6 +58,8 @@ _SIGNATURES = {
     "llmik_rope": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "llmik_rope_qkv_append_f16": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "llmik_add_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _p]),
+    "llmik_diag_empty": (_i, [_i, _p]),
+    "llmik_diag_read": (_i, [_p, _sz, _p, _i, _i, _p]),
     "llmik_silu_mul_halves": (_i, [_p, _p, _l, _i, _p]),
 }
 

@@ -1,0 +1,60 @@
+"""GPU checks of the measurement kernels (csrc/diag.hip) that bench.py
+--floors times: the plain read must read every byte once (the xor of the
+per-wave values equals the xor of every 32-bit word, computed on the CPU),
+at sizes that end inside a 4 KiB unit and at grids with more waves than
+units; the empty kernel must launch."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    from llmik_cuda._lib import check, lib
+    return lib, check
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("L", [4, 8, 16])
+@pytest.mark.parametrize("nbytes,nwg", [(16, 1), (4096, 2), (16000, 3), (40000, 1), (8_667_136, 256),
+                                        (30_314_496, 1024), (1 << 20, 2048)])
+def test_read_xor_covers_every_word(cuda, nbytes, nwg, L):
+    lib, check = _lib()
+    gen = torch.Generator(device=cuda).manual_seed(nbytes + nwg)
+    buf = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4 + 64,), generator=gen, device=cuda,
+                        dtype=torch.int32)   # 256 bytes past the range: must not be read
+    sink = torch.full((nwg * 8,), -1, dtype=torch.int32, device=cuda)
+    check(lib.llmik_diag_read(ctypes.c_void_p(buf.data_ptr()), nbytes,
+                              ctypes.c_void_p(sink.data_ptr()), nwg, L, _stream()))
+    torch.cuda.synchronize()
+    words = buf.cpu().numpy().view(np.uint32)[:nbytes // 4]
+    want = np.bitwise_xor.reduce(words) if words.size else np.uint32(0)
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    assert got == want
+
+
+def test_read_rejects_bad_arguments(cuda):
+    lib, _ = _lib()
+    buf = torch.zeros(1024, dtype=torch.int32, device=cuda)
+    sink = torch.zeros(8, dtype=torch.int32, device=cuda)
+    p, s = ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(sink.data_ptr())
+    assert lib.llmik_diag_read(p, 100, s, 1, 4, _stream()) != 0          # not a multiple of 16
+    assert lib.llmik_diag_read(ctypes.c_void_p(buf.data_ptr() + 4), 64, s, 1, 4, _stream()) != 0
+    assert lib.llmik_diag_read(p, 64, s, 0, 4, _stream()) != 0
+    assert lib.llmik_diag_read(p, 64, s, 1, 5, _stream()) != 0
+    assert lib.llmik_diag_empty(0, _stream()) != 0
+
+
+def test_empty_kernel_launches(cuda):
+    lib, check = _lib()
+    for nwg in (1, 256, 1024):
+        check(lib.llmik_diag_empty(nwg, _stream()))
+    torch.cuda.synchronize()
