@@ -127,6 +127,25 @@ def test_deterministic(llmik, cuda):
         assert torch.equal(first, llmik.w4a16_gemm(a, w, sc, 128))
 
 
+@pytest.mark.parametrize("M,K,N", [(128, 4096, 4096), (64, 4096, 4096), (128, 14336, 4096),
+                                   (300, 4096, 1024), (100, 384, 128), (40, 2048, 1152)])
+def test_split_gemm_repeatable(llmik, cuda, M, K, N):
+    """The M > 16 GEMM with K splits (the last split to arrive adds every
+    split's partial in split order, its own from registers): the same bits
+    over repeated calls in fp32 and fp16 out, fp32 within 2e-3 of the oracle.
+    Shapes: column tiles a multiple of 8 (a tile's splits on one XCD) and not
+    (its splits on several)."""
+    q, s, packed = _weights(K, N, 128, seed=M + K + N)
+    act = randn((M, K), M + 5).astype(np.float16)
+    a, w, sc = _dev(act, cuda), _dev(packed, cuda), _dev(s, cuda)
+    base = llmik.w4a16_gemm_f32out(a, w, sc, 128)
+    ref = ow.quantized_matmul_ref(act, q, s, 128, acc_dtype=np.float64)
+    assert np.abs(base.cpu().numpy() - ref).max() <= TOL
+    for _ in range(5):
+        assert torch.equal(llmik.w4a16_gemm_f32out(a, w, sc, 128), base)
+        assert torch.equal(llmik.w4a16_gemm(a, w, sc, 128), base.half())
+
+
 @pytest.mark.parametrize("K,N,gs", [(4096, 4096, 128), (256, 100, 64), (512, 36, 128)])
 def test_dequantize_bit_exact(llmik, cuda, K, N, gs):
     q, s, packed = _weights(K, N, gs, seed=K + 3)
