@@ -260,6 +260,28 @@ LLMIK_API llmik_status llmik_w4a16_gemm_f32out(
     int M, int N, int K, int group_size, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * A gate|up projection and its SwiGLU in one launch (the decode step's MLP;
+ * no single counterpart in the reference, which runs the gate and up
+ * QuantizedLinear projections and silu(gate) * up as separate ops,
+ * integration/prealloc_cache.py:129-130). weight_packed [K/8, N] / scale
+ * [K/g, N] hold the gate and up weights with their columns interleaved in
+ * 64-column tiles: tile t is gate columns 32t .. 32t+31, then up columns
+ * 32t .. 32t+31. out [M, N/2] fp16 gets fp16(silu(g) * u) of the
+ * fp16-rounded products g = (act @ W)[:, 64t + j], u = (act @ W)[:, 64t + 32 + j]
+ * at column 32t + j: the bits of llmik_w4a16_gemm on the concatenated
+ * weight followed by llmik_silu_mul_halves when both run the streaming
+ * GEMV. Needs 1 <= M <= 16, N % 64 == 0, K % 32 == 0 and a power-of-two
+ * group_size >= 32 (LLMIK_ERR_UNSUPPORTED otherwise); the workspace is
+ * llmik_w4a16_swiglu_workspace_size(M, N, K, group_size) bytes, with the
+ * rules of llmik_w4a16_gemm.
+ */
+LLMIK_API size_t llmik_w4a16_swiglu_workspace_size(int M, int N, int K, int group_size);
+LLMIK_API llmik_status llmik_w4a16_gemm_swiglu(const void* act, const void* weight_packed,
+                                               const void* scale, void* out, int M, int N, int K,
+                                               int group_size, void* workspace, size_t workspace_bytes,
+                                               void* stream);
+
+/*
  * Plan knobs of the W4A16 entry points, for measurement and tests (no
  * reference counterpart). stream_mode: 1 forces the streaming GEMV wherever
  * the shape allows, 0 disables it, -1 restores the size rule; stream_splits

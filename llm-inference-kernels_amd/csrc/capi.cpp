@@ -330,6 +330,21 @@ LLMIK_API llmik_status llmik_w4a16_gemm_f32out(const void* act, const void* weig
                         workspace_bytes, as_stream(stream));
 }
 
+LLMIK_API size_t llmik_w4a16_swiglu_workspace_size(int M, int N, int K, int group_size) {
+    return plan_w4a16_swiglu(M, N, K, group_size).workspace_bytes;
+}
+
+LLMIK_API llmik_status llmik_w4a16_gemm_swiglu(const void* act, const void* weight_packed,
+                                               const void* scale, void* out, int M, int N, int K,
+                                               int group_size, void* workspace, size_t workspace_bytes,
+                                               void* stream) {
+    int st = check_gemm(act, weight_packed, scale, out, M, N, K, group_size);
+    if (st != LLMIK_OK) return st;
+    if (M == 0 || N == 0) return LLMIK_OK;
+    return launch_w4a16_swiglu(act, weight_packed, scale, out, M, N, K, group_size, workspace,
+                               workspace_bytes, as_stream(stream));
+}
+
 LLMIK_API void llmik_w4a16_set_plan_override(int stream_mode, int stream_splits) {
     set_w4a16_plan_override(stream_mode, stream_splits);
 }

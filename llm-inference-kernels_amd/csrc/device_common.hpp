@@ -189,6 +189,12 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t n) {
     return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
 }
 
+// ---- SwiGLU ------------------------------------------------------------------
+// silu(g) * u of one element in fp32 (the decode step's MLP activation; the
+// elementwise kernels and the W4A16 SwiGLU epilogue share it, so both round
+// the same value).
+__device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 // ---- exact symmetric quantisation step ------------------------------------
 // Returns rint(x / s) with x / s the IEEE correctly rounded fp32 quotient,
 // which is what torch's CPU `x / scale` followed by `.round()` computes.

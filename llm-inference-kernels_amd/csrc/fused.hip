@@ -107,7 +107,6 @@ __global__ __launch_bounds__(256) void rmsnorm_regs_kernel(const uint16_t* __res
     }
 }
 
-__device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ g,
                                                        const uint16_t* __restrict__ u,

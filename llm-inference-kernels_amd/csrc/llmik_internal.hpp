@@ -95,6 +95,9 @@ struct GemmPlan {
 };
 
 GemmPlan plan_w4a16(int M, int N, int K, int group_size);
+GemmPlan plan_w4a16_swiglu(int M, int N, int K, int group_size);
+int launch_w4a16_swiglu(const void* act, const void* w, const void* scale, void* out, int M, int N,
+                        int K, int group_size, void* ws, size_t ws_bytes, hipStream_t stream);
 int launch_w4a16(const void* act, const void* w, const void* scale, void* out, bool f32_out,
                  int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
                  hipStream_t stream);

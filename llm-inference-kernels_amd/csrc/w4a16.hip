@@ -42,6 +42,7 @@ struct GemmParams {
     int wave_steps;      // streaming GEMV / 32x32 GEMM: 32-K steps per wave
     int m_tiles_;        // 32x32 GEMM: row tiles
     int vec_out;         // 32x32 GEMM: out is 16-byte aligned (vector stores)
+    int swiglu;          // streaming GEMV: SwiGLU epilogue (see store_swiglu)
 };
 
 // Eight int4 codes of one word -> four fp16 pairs, exact. Pair j holds the
@@ -114,6 +115,15 @@ __device__ __forceinline__ void store_out(const GemmParams& p, int m, int n, flo
     } else {
         static_cast<uint16_t*>(p.out)[(long)m * p.N + n] = f2h_bits(v);
     }
+}
+
+// SwiGLU epilogue of the streaming GEMV. The weight's columns come in 64-column
+// tiles of 32 gate columns followed by the matching 32 up columns; column c of
+// the [M, N / 2] fp16 output is silu(g) * u of the fp16-rounded gate and up
+// products, the same value an fp16 gate|up product followed by silu_mul rounds.
+__device__ __forceinline__ void store_swiglu(const GemmParams& p, int m, int c, float g, float u) {
+    const float gh = h2f(f2h_bits(g)), uh = h2f(f2h_bits(u));
+    static_cast<uint16_t*>(p.out)[(long)m * (p.N / 2) + c] = f2h_bits(silu_mul1(gh, uh));
 }
 
 // 4 consecutive outputs of row m from column n (a multiple of 4): one 16- /
@@ -760,8 +770,17 @@ __global__ __launch_bounds__(kStreamMaxWaves * kWave) void w4a16_gemv_stream_ker
         for (int w = 0; w < nslots; ++w) v += s_red[w][o / TN][o % TN];
         return v;
     };
+    constexpr int TH = TN / 2;
+    const int nhalf = min(p.M, MR) * TH;   // SwiGLU outputs of the tile
     if (p.splits == 1) {
-        for (int o = t; o < nout; o += nthreads) store_out(p, o / TN, n0 + o % TN, tile_sum(o));
+        if (p.swiglu) {
+            for (int o = t; o < nhalf; o += nthreads) {
+                const int row = o / TH, j = o % TH;
+                store_swiglu(p, row, n0 / 2 + j, tile_sum(row * TN + j), tile_sum(row * TN + TH + j));
+            }
+        } else {
+            for (int o = t; o < nout; o += nthreads) store_out(p, o / TN, n0 + o % TN, tile_sum(o));
+        }
         return;
     }
     for (int o = t; o < nout; o += nthreads)
@@ -771,10 +790,19 @@ __global__ __launch_bounds__(kStreamMaxWaves * kWave) void w4a16_gemv_stream_ker
     if (t == 0) s_last = arrive_last(&p.counters[tile], (uint32_t)p.splits) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
-    for (int o = t; o < nout; o += nthreads) {
-        const int row = o / TN, col = o % TN;
-        store_out(p, row, n0 + col,
-                  sum_splits(p.part + (long)row * p.N + n0 + col, (long)p.M * p.N, p.splits));
+    if (p.swiglu) {
+        for (int o = t; o < nhalf; o += nthreads) {
+            const int row = o / TH, j = o % TH;
+            const float* base = p.part + (long)row * p.N + n0;
+            store_swiglu(p, row, n0 / 2 + j, sum_splits(base + j, (long)p.M * p.N, p.splits),
+                         sum_splits(base + TH + j, (long)p.M * p.N, p.splits));
+        }
+    } else {
+        for (int o = t; o < nout; o += nthreads) {
+            const int row = o / TN, col = o % TN;
+            store_out(p, row, n0 + col,
+                      sum_splits(p.part + (long)row * p.N + n0 + col, (long)p.M * p.N, p.splits));
+        }
     }
     if (t == 0) p.counters[tile] = 0u;
 }
@@ -1768,10 +1796,11 @@ void set_w4a16_plan_override(int stream_mode, int stream_splits) {
 static int stream_override() { return g_stream_mode.load(std::memory_order_relaxed); }
 static int stream_splits_override() { return g_stream_splits.load(std::memory_order_relaxed); }
 
-GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
+// stream_mode: 1 forces the streaming GEMV where its shape rule holds, 0 rules
+// it out, -1 applies the size rule.
+static GemmPlan plan_w4a16_mode(int M, int N, int K, int group_size, int stream_mode) {
     GemmPlan pl{};
     const bool pow2_group = group_size >= 32 && (group_size & (group_size - 1)) == 0;
-    const int stream_mode = stream_override();
     const bool stream_size_ok = (long)K * N / 2 > kStreamMinWeightBytes;
     if (M >= 1 && M <= 16 && N % 64 == 0 && pow2_group && K % 32 == 0 &&
         (long)(K / 8) * N * 4 < (1L << 31) && (long)M * K * 2 < (1L << 31) &&
@@ -1964,15 +1993,25 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     return pl;
 }
 
-int launch_w4a16(const void* act, const void* w, const void* scale, void* out, bool f32_out,
-                 int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
-                 hipStream_t stream) {
-    if (M == 0 || N == 0) return LLMIK_OK;
-    const GemmPlan pl = plan_w4a16(M, N, K, group_size);
-    if (pl.splits > 1 && ws_bytes < pl.workspace_bytes)
-        return set_error(LLMIK_ERR_WORKSPACE, "workspace too small for this W4A16 call");
-    if (pl.m_tiles > 65535 || pl.splits > 65535)
-        return set_error(LLMIK_ERR_UNSUPPORTED, "W4A16 grid too large");
+GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
+    return plan_w4a16_mode(M, N, K, group_size, stream_override());
+}
+
+// The SwiGLU form always runs the streaming GEMV (its epilogue pairs the two
+// 32-column halves of each 64-column tile), so it needs that kernel's shape.
+static bool swiglu_shape_ok(int M, int N, int K, int group_size) {
+    const bool pow2_group = group_size >= 32 && (group_size & (group_size - 1)) == 0;
+    return M >= 1 && M <= 16 && N > 0 && N % 64 == 0 && K > 0 && K % 32 == 0 && pow2_group &&
+           (long)(K / 8) * N * 4 < (1L << 31) && (long)M * K * 2 < (1L << 31);
+}
+
+GemmPlan plan_w4a16_swiglu(int M, int N, int K, int group_size) {
+    if (!swiglu_shape_ok(M, N, K, group_size)) return GemmPlan{};
+    return plan_w4a16_mode(M, N, K, group_size, 1);
+}
+
+static GemmParams gemm_params(const GemmPlan& pl, const void* act, const void* w, const void* scale,
+                              void* out, bool f32_out, int M, int N, int K, int group_size, void* ws) {
     GemmParams p{};
     p.act = static_cast<const uint16_t*>(act);
     p.w = static_cast<const uint32_t*>(w);
@@ -1990,6 +2029,37 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
     while ((32 << p.gshift) < group_size) ++p.gshift;
     p.nw = pl.waves;
     p.wave_steps = pl.wave_steps;
+    return p;
+}
+
+int launch_w4a16_swiglu(const void* act, const void* w, const void* scale, void* out, int M, int N,
+                        int K, int group_size, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!swiglu_shape_ok(M, N, K, group_size))
+        return set_error(LLMIK_ERR_UNSUPPORTED,
+                         "w4a16 SwiGLU needs 1 <= M <= 16, N % 64 == 0, K % 32 == 0 and a power-of-two "
+                         "group_size >= 32");
+    const GemmPlan pl = plan_w4a16_swiglu(M, N, K, group_size);
+    if (pl.kind != 5) return set_error(LLMIK_ERR_UNSUPPORTED, "w4a16 SwiGLU: no streaming plan");
+    if (pl.splits > 1 && ws_bytes < pl.workspace_bytes)
+        return set_error(LLMIK_ERR_WORKSPACE, "workspace too small for this W4A16 call");
+    GemmParams p = gemm_params(pl, act, w, scale, out, false, M, N, K, group_size, ws);
+    p.swiglu = 1;
+    const int grid = pl.n_tiles * pl.splits;
+    if (M == 1) launch_stream<1>(p, grid, stream);
+    else launch_stream<16>(p, grid, stream);
+    return check_launch();
+}
+
+int launch_w4a16(const void* act, const void* w, const void* scale, void* out, bool f32_out,
+                 int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
+                 hipStream_t stream) {
+    if (M == 0 || N == 0) return LLMIK_OK;
+    const GemmPlan pl = plan_w4a16(M, N, K, group_size);
+    if (pl.splits > 1 && ws_bytes < pl.workspace_bytes)
+        return set_error(LLMIK_ERR_WORKSPACE, "workspace too small for this W4A16 call");
+    if (pl.m_tiles > 65535 || pl.splits > 65535)
+        return set_error(LLMIK_ERR_UNSUPPORTED, "W4A16 grid too large");
+    GemmParams p = gemm_params(pl, act, w, scale, out, f32_out, M, N, K, group_size, ws);
     dim3 block(kGemmThreads);
     if (pl.kind == 5) {
         const int grid = pl.n_tiles * pl.splits;

@@ -347,6 +347,31 @@ Tensor w4a16_gemm(const Tensor& act, const Tensor& weight_packed, const Tensor& 
     return gemm(act, weight_packed, scale, group_size, false);
 }
 
+Tensor w4a16_gemm_swiglu(const Tensor& act, const Tensor& weight_packed, const Tensor& scale, int64_t group_size) {
+    TORCH_CHECK(act.scalar_type() == at::kHalf, "act must be fp16");
+    TORCH_CHECK(weight_packed.scalar_type() == at::kInt, "weight_packed must be int32 (uint32 bit pattern)");
+    TORCH_CHECK(scale.scalar_type() == at::kHalf, "scale must be fp16");
+    TORCH_CHECK(act.is_contiguous() && weight_packed.is_contiguous() && scale.is_contiguous(),
+                "all tensors must be contiguous");
+    TORCH_CHECK(act.dim() == 2 && weight_packed.dim() == 2 && scale.dim() == 2, "all inputs must be 2D");
+    const int M = act.size(0), K = act.size(1);
+    const int N = weight_packed.size(1);
+    TORCH_CHECK(K == weight_packed.size(0) * 8, "act.K must equal weight_packed.K_packs * 8");
+    TORCH_CHECK(scale.size(1) == N, "scale and weight_packed N mismatch");
+    TORCH_CHECK(group_size > 0 && group_size % 8 == 0, "group_size must be a positive multiple of 8");
+    TORCH_CHECK(K == scale.size(0) * group_size, "K must equal n_groups * group_size");
+    TORCH_CHECK(N % 64 == 0, "the interleaved gate|up weight needs N % 64 == 0");
+    TORCH_CHECK(act.is_cuda() && weight_packed.is_cuda() && scale.is_cuda(), "all inputs must be CUDA tensors");
+    const c10::DeviceGuard guard(act.device());
+    Tensor out = at::empty({M, N / 2}, act.options());
+    if (M == 0) return out;
+    const hipStream_t st = stream_of(act);
+    auto ws = workspace(act, st, llmik_w4a16_swiglu_workspace_size(M, N, K, (int)group_size));
+    check(llmik_w4a16_gemm_swiglu(ptr(act), ptr(weight_packed), ptr(scale), ptr(out), M, N, K, (int)group_size,
+                                  ws.first, ws.second, st));
+    return out;
+}
+
 Tensor w4a16_gemm_f32out(const Tensor& act, const Tensor& weight_packed, const Tensor& scale, int64_t group_size) {
     return gemm(act, weight_packed, scale, group_size, true);
 }
@@ -486,6 +511,7 @@ PYBIND11_MODULE(_C, m) {
     m.def("kivi_append_token_int4", &kivi_append_token_int4);
     m.def("w4a16_gemm", &w4a16_gemm);
     m.def("w4a16_gemm_f32out", &w4a16_gemm_f32out);
+    m.def("w4a16_gemm_swiglu", &w4a16_gemm_swiglu);
     m.def("w4a16_dequantize", &w4a16_dequantize);
     m.def("rmsnorm", &rmsnorm);
     m.def("silu_mul", &silu_mul);

@@ -48,7 +48,7 @@ __all__ = [
     "w4a16_gemm_f32out", "quantize_per_token_into", "quantize_v_per_token_int4_into",
     "quantize_k_per_channel_groupwise_int4_into", "quantize_weights_int4_groupwise",
     "pack_int4_along_k", "quantize_pack_weights_int4", "kivi_append_token_int4", "rope_qkv_append", "add_rmsnorm", "silu_mul_halves",
-    "LIB_PATH",
+    "w4a16_gemm_swiglu", "interleave_gate_up", "LIB_PATH",
 ]
 
 
@@ -251,6 +251,31 @@ def w4a16_gemm_f32out(act: torch.Tensor, weight_packed: torch.Tensor, scale: tor
     _require(_is_device(act) and _is_device(weight_packed) and _is_device(scale),
                  "all inputs must be CUDA tensors")
     return _C.w4a16_gemm_f32out(act, weight_packed, scale, int(group_size))
+
+
+def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """The column order `w4a16_gemm_swiglu` expects, from the gate and up
+    weights [K, I] (any dtype, I % 32 == 0): [K, 2 I] in 64-column tiles of
+    32 gate columns followed by the same 32 up columns. Quantising it column
+    by column gives each column the codes and scales it has in the separate
+    weights."""
+    _require(gate.shape == up.shape and gate.dim() == 2 and gate.shape[1] % 32 == 0,
+             "gate and up must be [K, I] with I % 32 == 0")
+    K, inter = gate.shape
+    return torch.stack((gate.reshape(K, inter // 32, 32), up.reshape(K, inter // 32, 32)),
+                       dim=2).reshape(K, 2 * inter)
+
+
+def w4a16_gemm_swiglu(act: torch.Tensor, weight_packed: torch.Tensor, scale: torch.Tensor,
+                      group_size: int) -> torch.Tensor:
+    """The decode step's gate|up projection and SwiGLU in one launch:
+    out [M, N/2] fp16 = silu(g) * up for a weight whose columns are
+    `interleave_gate_up(gate, up)` (packed [K/8, N], scale [K/g, N]), with
+    g and up the fp16 products (prealloc_cache.py:129-130: silu_mul of the
+    gate and up projections). 1 <= M <= 16, N % 64 == 0."""
+    _require(_is_device(act) and _is_device(weight_packed) and _is_device(scale),
+             "all inputs must be CUDA tensors")
+    return _C.w4a16_gemm_swiglu(act, weight_packed, scale, int(group_size))
 
 
 def w4a16_dequantize(weight_packed: torch.Tensor, scale: torch.Tensor,

@@ -13,12 +13,14 @@ projections are W4A16 `QuantizedLinear`s (integration/w4a16_patch.py:67-116).
     h = x + o_proj(decode_attention(q, kbuf, vbuf, scale, pos + 1))
     out = h + down_proj(silu_mul(gate_proj(n2), up_proj(n2))),  n2 = rmsnorm(h)
 
-With `fused=True` (the default) the step makes 10 launches instead of 17:
-q|k|v and gate|up are each one W4A16 projection over column-concatenated
-weights (codes and scales per column are those of the separate matrices),
-`rope_qkv_append` ropes q and k and writes the cache slot, `add_rmsnorm`
-takes the residual add and the second norm, and `silu_mul_halves` reads the
-fused gate|up output. `fused=False` runs the op-by-op sequence above.
+With `fused=True` (the default) the step makes 9 launches instead of 17:
+q|k|v is one W4A16 projection over column-concatenated weights (codes and
+scales per column are those of the separate matrices), `rope_qkv_append`
+ropes q and k and writes the cache slot, `add_rmsnorm` takes the residual add
+and the second norm, and gate|up with its SwiGLU is one launch
+(`w4a16_gemm_swiglu` over the gate and up columns interleaved in 64-column
+tiles; batches above 16 rows keep the concatenated gate|up projection and
+`silu_mul_halves`). `fused=False` runs the op-by-op sequence above.
 `DecodeStack` runs merged layers in sequence with each layer's last residual
 add carried into the next layer's first RMSNorm launch.
 
@@ -36,8 +38,8 @@ from typing import Dict, Optional, Tuple
 
 import torch
 
-from . import (add_rmsnorm, decode_attention, quantize_pack_weights_int4, rmsnorm, rope,
-               rope_qkv_append, silu_mul, silu_mul_halves, w4a16_gemm)
+from . import (add_rmsnorm, decode_attention, interleave_gate_up, quantize_pack_weights_int4, rmsnorm,
+               rope, rope_qkv_append, silu_mul, silu_mul_halves, w4a16_gemm, w4a16_gemm_swiglu)
 
 
 class W4Linear:
@@ -53,6 +55,10 @@ class W4Linear:
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         return w4a16_gemm(x, self.weight_packed, self.scale, self.group_size)
+
+    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+        """silu(gate) * up of a weight built from `interleave_gate_up`."""
+        return w4a16_gemm_swiglu(x, self.weight_packed, self.scale, self.group_size)
 
 
 def rope_tables(max_len: int, head_dim: int, theta: float, device: torch.device) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -72,8 +78,11 @@ class DecodeLayer:
     ln1, ln2 to [hidden] fp16 vectors; missing entries are drawn from a seeded
     generator (N(0, 0.02) matrices, N(1, 0.1) norm weights). Only the packed
     codes and fp16 scales of the matrices are kept: in `proj` under their
-    names, or with `fused=True` as "qkv" and "gate_up" column concatenations;
-    `columns[name]` gives (key in `proj`, first column, end column)."""
+    names, or with `fused=True` as "qkv" and "gate_up" column concatenations
+    (gate|up interleaved in 64-column tiles when the SwiGLU launch applies);
+    `columns[name]` gives (key in `proj`, the indices of the columns of that
+    projection's output, in order). `merge_swiglu=False` keeps the merged
+    step's gate|up projection and `silu_mul_halves` as two launches."""
 
     NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
@@ -81,7 +90,7 @@ class DecodeLayer:
                  max_len: int, device: Optional[torch.device] = None, head_dim: int = 128,
                  group_size: int = 128, eps: float = 1e-5, rope_theta: float = 500000.0,
                  weights: Optional[Dict[str, torch.Tensor]] = None, seed: int = 0,
-                 fused: bool = True) -> None:
+                 fused: bool = True, merge_swiglu: bool = True) -> None:
         if n_heads * head_dim != hidden or n_heads % n_kv_heads != 0:
             raise RuntimeError("hidden must be n_heads * head_dim and n_heads a multiple of n_kv_heads")
         dev = torch.device("cuda") if device is None else torch.device(device)
@@ -102,18 +111,30 @@ class DecodeLayer:
                 weights[name] = (1.0 + 0.1 * torch.randn(hidden, generator=gen, device=dev)).half()
         # the merged kernels' limits: add_rmsnorm rows of at most 8192, 16-byte vectors
         self.fused = fused and hidden % 8 == 0 and hidden <= 8192 and intermediate % 8 == 0
+        # gate|up + SwiGLU in one launch: the streaming GEMV's rows and tiles
+        self.swiglu = (self.fused and merge_swiglu and batch <= 16 and intermediate % 32 == 0
+                       and group_size >= 32 and group_size & (group_size - 1) == 0)
+        span = lambda a, b: torch.arange(a, b)  # noqa: E731
         if self.fused:
             cat = lambda *ns: torch.cat([weights.pop(n) for n in ns], dim=1)  # noqa: E731
             self.proj = {"qkv": W4Linear(cat("q", "k", "v"), group_size), "o": W4Linear(weights.pop("o"), group_size),
-                         "gate_up": W4Linear(cat("gate", "up"), group_size),
                          "down": W4Linear(weights.pop("down"), group_size)}
-            self.columns = {"q": ("qkv", 0, hidden), "k": ("qkv", hidden, hidden + kv),
-                            "v": ("qkv", hidden + kv, hidden + 2 * kv), "o": ("o", 0, hidden),
-                            "gate": ("gate_up", 0, intermediate),
-                            "up": ("gate_up", intermediate, 2 * intermediate), "down": ("down", 0, hidden)}
+            self.columns = {"q": ("qkv", span(0, hidden)), "k": ("qkv", span(hidden, hidden + kv)),
+                            "v": ("qkv", span(hidden + kv, hidden + 2 * kv)), "o": ("o", span(0, hidden)),
+                            "down": ("down", span(0, hidden))}
+            if self.swiglu:
+                self.proj["gate_up"] = W4Linear(interleave_gate_up(weights.pop("gate"), weights.pop("up")),
+                                                group_size)
+                gate_cols = (span(0, intermediate) // 32) * 64 + span(0, intermediate) % 32
+                self.columns["gate"] = ("gate_up", gate_cols)
+                self.columns["up"] = ("gate_up", gate_cols + 32)
+            else:
+                self.proj["gate_up"] = W4Linear(cat("gate", "up"), group_size)
+                self.columns["gate"] = ("gate_up", span(0, intermediate))
+                self.columns["up"] = ("gate_up", span(intermediate, 2 * intermediate))
         else:
             self.proj = {name: W4Linear(weights.pop(name), group_size) for name in self.NAMES}
-            self.columns = {name: (name, 0, shapes[name][1]) for name in self.NAMES}
+            self.columns = {name: (name, span(0, shapes[name][1])) for name in self.NAMES}
         self.ln1 = weights["ln1"].to(dev, torch.float16).contiguous()
         self.ln2 = weights["ln2"].to(dev, torch.float16).contiguous()
         self.cos, self.sin = rope_tables(max_len, head_dim, rope_theta, dev)
@@ -169,7 +190,8 @@ class DecodeLayer:
         q = rope_qkv_append(p["qkv"](n1), self.cos[pos], self.sin[pos], self.kbuf, self.vbuf, pos)
         attn = decode_attention(q, self.kbuf, self.vbuf, self.scale, pos + 1)
         h, n2 = add_rmsnorm(x, p["o"](attn.view(B, H * D)), self.ln2, self.eps)
-        return h, p["down"](silu_mul_halves(p["gate_up"](n2)))
+        act = p["gate_up"].swiglu(n2) if self.swiglu else silu_mul_halves(p["gate_up"](n2))
+        return h, p["down"](act)
 
     def capture(self, x: torch.Tensor, pos: int, warmup: int = 2) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
         """Record `step(x, pos)` in a CUDA (HIP) graph. Returns the graph and
@@ -182,7 +204,8 @@ class DecodeLayer:
 class DecodeStack:
     """Merged-step layers run in sequence for one token. Layer i's last
     residual add goes into layer i + 1's first RMSNorm launch
-    (`step_parts(..., residual=)`), so n layers make 9 n + 1 launches; the
+    (`step_parts(..., residual=)`), so n layers make 8 n + 1 launches (9 n + 1
+    without the gate|up SwiGLU launch); the
     output equals chaining `layer.step` bit for bit (the merged norm rounds
     x + residual exactly as the add it replaces)."""
 

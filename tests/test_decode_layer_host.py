@@ -44,3 +44,21 @@ def test_stack_needs_merged_layers():
     with pytest.raises(RuntimeError, match="fused=True"):
         DecodeStack([_Layer(True), _Layer(False)])
     assert len(DecodeStack([_Layer(True), _Layer(True)]).layers) == 2
+
+
+def test_interleave_gate_up_tiles():
+    """64-column tiles of 32 gate columns then the same 32 up columns; the
+    column indices DecodeLayer records for gate and up pick them back out."""
+    import llmik_cuda
+    K, inter = 3, 96
+    gate = torch.arange(K * inter, dtype=torch.float32).reshape(K, inter)
+    up = -gate - 1
+    w = llmik_cuda.interleave_gate_up(gate, up)
+    assert w.shape == (K, 2 * inter)
+    for t in range(inter // 32):
+        assert torch.equal(w[:, 64 * t:64 * t + 32], gate[:, 32 * t:32 * t + 32])
+        assert torch.equal(w[:, 64 * t + 32:64 * t + 64], up[:, 32 * t:32 * t + 32])
+    cols = (torch.arange(inter) // 32) * 64 + torch.arange(inter) % 32
+    assert torch.equal(w[:, cols], gate) and torch.equal(w[:, cols + 32], up)
+    with pytest.raises(RuntimeError, match="I % 32"):
+        llmik_cuda.interleave_gate_up(gate[:, :40], up[:, :40])

@@ -47,11 +47,11 @@ def _x(cuda, seed):
 
 
 def _w_hat(layer, name) -> np.ndarray:
-    key, a, b = layer.columns[name]
+    key, cols = layer.columns[name]
     lin = layer.proj[key]
     codes = ow.unpack_int4_along_k(lin.weight_packed.cpu().numpy())
     w = ow.dequantize_weights_int4_groupwise(codes, lin.scale.cpu().numpy(), lin.group_size)
-    return w[:, a:b]
+    return w[:, cols.numpy()]
 
 
 def _h(a: np.ndarray) -> np.ndarray:

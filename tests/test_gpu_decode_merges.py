@@ -1,7 +1,8 @@
 """GPU: the decode-step merges (rope_qkv_append, add_rmsnorm,
-silu_mul_halves) give the same bits as the ops they replace, which the fused
-op tests pin against the fp32 oracle; add_rmsnorm is also checked against the
-oracle directly."""
+silu_mul_halves, w4a16_gemm_swiglu) give the same bits as the ops they
+replace, which the fused op and W4A16 tests pin against the fp32 oracle;
+add_rmsnorm and w4a16_gemm_swiglu are also checked against the oracle
+directly."""
 from __future__ import annotations
 
 import numpy as np
@@ -9,6 +10,7 @@ import pytest
 import torch
 
 from oracle import fused as of
+from oracle import w4a16 as ow
 from tests.helpers import randn
 
 pytestmark = pytest.mark.gpu
@@ -83,3 +85,53 @@ def test_merges_reject_bad_shapes(llmik, cuda):
         llmik.add_rmsnorm(x, x, x[0], 1e-5)
     with pytest.raises(RuntimeError, match="multiple of 8"):
         llmik.silu_mul_halves(torch.zeros((2, 24), dtype=torch.float16, device=cuda))
+
+
+@pytest.mark.parametrize("M,K,inter", [(8, 4096, 14336), (1, 4096, 14336), (16, 512, 1024), (3, 256, 96),
+                                       (8, 14336, 2048), (5, 1024, 4096)])
+def test_w4a16_gemm_swiglu_equals_gemm_then_silu_mul_halves(llmik, cuda, M, K, inter):
+    """gate|up + SwiGLU in one launch over the interleaved weight gives the
+    bits of the gate|up product over the concatenated weight (on the same
+    streaming GEMV plan) followed by silu_mul_halves. Against the oracle
+    (silu_mul of the float64 gate and up products g, u): the fp16 gate and up
+    products are each within one fp16 ulp + 2e-3 of g and u (the W4A16
+    gate), so the output is within |u| silu'(g) (ulp(g) + 2e-3) + |silu(g)|
+    (ulp(u) + 2e-3) + one fp16 ulp of the result. Shapes: the Llama gate|up
+    at M = 8 and 1, K splits, 96 columns (three tile pairs), the
+    down-projection K."""
+    from llmik_cuda._lib import lib
+    gen = torch.Generator(device=cuda).manual_seed(M * 31 + K + inter)
+    gate = torch.randn((K, inter), generator=gen, device=cuda) * 0.02
+    up = torch.randn((K, inter), generator=gen, device=cuda) * 0.02
+    wc, sc_c = llmik.quantize_pack_weights_int4(torch.cat([gate, up], dim=1).contiguous(), 128)
+    wi, sc_i = llmik.quantize_pack_weights_int4(llmik.interleave_gate_up(gate, up).contiguous(), 128)
+    act = torch.randn((M, K), generator=gen, device=cuda).half()
+    out = llmik.w4a16_gemm_swiglu(act, wi, sc_i, 128)
+    assert out.shape == (M, inter) and out.dtype == torch.float16
+    lib.llmik_w4a16_set_plan_override(1, -1)   # the concatenated product on the streaming GEMV too
+    try:
+        ref = llmik.silu_mul_halves(llmik.w4a16_gemm(act, wc, sc_c, 128))
+    finally:
+        lib.llmik_w4a16_set_plan_override(-1, -1)
+    assert torch.equal(out, ref)
+    assert torch.equal(llmik.w4a16_gemm_swiglu(act, wi, sc_i, 128), out)   # repeatable
+    codes = ow.unpack_int4_along_k(wc.cpu().numpy())
+    w = ow.dequantize_weights_int4_groupwise(codes, sc_c.cpu().numpy(), 128).astype(np.float64)
+    a = act.cpu().numpy().astype(np.float64)
+    g, u = a @ w[:, :inter], a @ w[:, inter:]
+    sg = 1.0 / (1.0 + np.exp(-g))
+    want = g * sg * u
+    ulp = lambda x: np.spacing(np.abs(x).astype(np.float16)).astype(np.float64)  # noqa: E731
+    dsilu = np.abs(sg * (1.0 + g * (1.0 - sg)))
+    tol = np.abs(u) * dsilu * (ulp(g) + 2e-3) + np.abs(g * sg) * (ulp(u) + 2e-3) + ulp(want)
+    assert (np.abs(out.cpu().numpy().astype(np.float64) - want) <= tol).all()
+
+
+def test_w4a16_gemm_swiglu_rejects_unsupported_shapes(llmik, cuda):
+    act = torch.zeros((17, 256), dtype=torch.float16, device=cuda)
+    w = torch.zeros((32, 128), dtype=torch.int32, device=cuda)
+    s = torch.ones((2, 128), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="M <= 16"):
+        llmik.w4a16_gemm_swiglu(act, w, s, 128)
+    with pytest.raises(RuntimeError, match="N % 64"):
+        llmik.w4a16_gemm_swiglu(act[:4], w[:, :96].contiguous(), s[:, :96].contiguous(), 128)
