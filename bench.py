@@ -293,7 +293,7 @@ def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmu
     rmsnorm, W4A16 q/k/v/o/gate/up/down, rope, fp16 cache write, split-K
     attention over `ctx` tokens, silu_mul, residual adds), launched eagerly
     from Python and replayed from one HIP graph; `fused` picks the merged
-    step (a DecodeStack: 8 launches per layer plus one) or the op-by-op
+    step (a DecodeStack: 7 launches per layer plus one) or the op-by-op
     17-launch one. Four layers hold ~950 MB of weights and caches, so the
     replays read HBM, not the Infinity Cache."""
     import torch

@@ -282,6 +282,31 @@ LLMIK_API llmik_status llmik_w4a16_gemm_swiglu(const void* act, const void* weig
                                                void* stream);
 
 /*
+ * The decode step's q|k|v projection, its rope and the cache append in one
+ * launch (head_dim 128): llmik_w4a16_gemm over the concatenated q | k | v
+ * weight followed by llmik_rope_qkv_append_f16, with the same bits when both
+ * run the streaming GEMV. No single counterpart in the reference, which runs
+ * the q, k and v QuantizedLinear projections, rope of q and k and the cache
+ * update as separate ops (integration/prealloc_cache.py:42-110,132-133).
+ * weight_packed [K/8, N] / scale [K/g, N], N = (n_heads + 2 n_kv_heads) 128,
+ * hold the concatenated weight with each head's two 64-dimension halves
+ * interleaved in 32-column blocks: the head's columns are dimensions 0..31,
+ * 64..95, 32..63, 96..127. cos / sin are the position's [128] fp16 rotary
+ * rows; q_out [batch, n_heads, 128] gets the roped q, slot `pos` of k_cache /
+ * v_cache [batch, n_kv_heads, max_len, 128] the roped k and v. Needs
+ * 1 <= batch <= 16, K % 32 == 0 and a power-of-two group_size >= 32
+ * (LLMIK_ERR_UNSUPPORTED otherwise); workspace of
+ * llmik_w4a16_qkv_rope_workspace_size(...) bytes, with the rules of
+ * llmik_w4a16_gemm.
+ */
+LLMIK_API size_t llmik_w4a16_qkv_rope_workspace_size(int batch, int n_heads, int n_kv_heads, int K,
+                                                     int group_size);
+LLMIK_API llmik_status llmik_w4a16_gemm_qkv_rope_f16(
+    const void* act, const void* weight_packed, const void* scale, const void* cos, const void* sin,
+    void* q_out, void* k_cache, void* v_cache, int batch, int K, int group_size, int n_heads,
+    int n_kv_heads, int max_len, int pos, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Plan knobs of the W4A16 entry points, for measurement and tests (no
  * reference counterpart). stream_mode: 1 forces the streaming GEMV wherever
  * the shape allows, 0 disables it, -1 restores the size rule; stream_splits

@@ -331,7 +331,32 @@ LLMIK_API llmik_status llmik_w4a16_gemm_f32out(const void* act, const void* weig
 }
 
 LLMIK_API size_t llmik_w4a16_swiglu_workspace_size(int M, int N, int K, int group_size) {
-    return plan_w4a16_swiglu(M, N, K, group_size).workspace_bytes;
+    return plan_w4a16_stream_forced(M, N, K, group_size).workspace_bytes;
+}
+
+LLMIK_API size_t llmik_w4a16_qkv_rope_workspace_size(int batch, int n_heads, int n_kv_heads, int K,
+                                                     int group_size) {
+    if (n_heads <= 0 || n_kv_heads <= 0) return 0;
+    return plan_w4a16_stream_forced(batch, (n_heads + 2 * n_kv_heads) * 128, K, group_size).workspace_bytes;
+}
+
+LLMIK_API llmik_status llmik_w4a16_gemm_qkv_rope_f16(
+    const void* act, const void* weight_packed, const void* scale, const void* cos, const void* sin,
+    void* q_out, void* k_cache, void* v_cache, int batch, int K, int group_size, int n_heads,
+    int n_kv_heads, int max_len, int pos, void* workspace, size_t workspace_bytes, void* stream) {
+    if (batch < 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
+        return invalid("n_heads must be a positive multiple of n_kv_heads");
+    if (pos < 0 || pos >= max_len) return invalid("pos outside the cache");
+    const int N = (n_heads + 2 * n_kv_heads) * 128;
+    int st = check_gemm(act, weight_packed, scale, q_out, batch, N, K, group_size);
+    if (st != LLMIK_OK) return st;
+    if (!cos || !sin || !k_cache || !v_cache) return invalid("null pointer");
+    if (!aligned(cos, 2) || !aligned(sin, 2) || !aligned(k_cache, 2) || !aligned(v_cache, 2))
+        return set_error(LLMIK_ERR_ALIGNMENT, "cos, sin and the caches must be 2-byte aligned");
+    if (batch == 0) return LLMIK_OK;
+    return launch_w4a16_qkv_rope(act, weight_packed, scale, cos, sin, q_out, k_cache, v_cache, batch, K,
+                                 group_size, n_heads, n_kv_heads, max_len, pos, workspace,
+                                 workspace_bytes, as_stream(stream));
 }
 
 LLMIK_API llmik_status llmik_w4a16_gemm_swiglu(const void* act, const void* weight_packed,

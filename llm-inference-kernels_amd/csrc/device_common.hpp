@@ -195,6 +195,18 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t n) {
 // the same value).
 __device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+// ---- rotary embedding ---------------------------------------------------------
+// The rotation of one pair (x[d], x[d + D/2]): rotate_half(x) = [-x[D/2:],
+// x[:D/2]], so out[d] = x1 c1 - x2 s1 and out[d + D/2] = x2 c2 + x1 s2. The
+// fma is written out once here so that every kernel using it (rope, the
+// decode step's rope + cache append, the W4A16 q|k|v epilogue) rounds the
+// same way.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c1, float s1, float c2, float s2,
+                                          uint16_t& o1, uint16_t& o2) {
+    o1 = f2h_bits(fmaf(x1, c1, -(x2 * s1)));
+    o2 = f2h_bits(fmaf(x2, c2, x1 * s2));
+}
+
 // ---- exact symmetric quantisation step ------------------------------------
 // Returns rint(x / s) with x / s the IEEE correctly rounded fp32 quotient,
 // which is what torch's CPU `x / scale` followed by `.round()` computes.

@@ -127,15 +127,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
     }
 }
 
-// The rotation of one pair (x[d], x[d + D/2]): rotate_half(x) = [-x[D/2:],
-// x[:D/2]], so out[d] = x1 c1 - x2 s1 and out[d + D/2] = x2 c2 + x1 s2. The
-// fma is written out so that every kernel using it rounds the same way.
-__device__ __forceinline__ void rope_pair(float x1, float x2, float c1, float s1, float c2, float s2,
-                                          uint16_t& o1, uint16_t& o2) {
-    o1 = f2h_bits(fmaf(x1, c1, -(x2 * s1)));
-    o2 = f2h_bits(fmaf(x2, c2, x1 * s2));
-}
-
 // One thread per (b, h, s, d) with d < D/2: it produces out[d] and
 // out[d + D/2] from the pair (x[d], x[d + D/2]).
 __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ x,

@@ -95,9 +95,13 @@ struct GemmPlan {
 };
 
 GemmPlan plan_w4a16(int M, int N, int K, int group_size);
-GemmPlan plan_w4a16_swiglu(int M, int N, int K, int group_size);
+GemmPlan plan_w4a16_stream_forced(int M, int N, int K, int group_size);
 int launch_w4a16_swiglu(const void* act, const void* w, const void* scale, void* out, int M, int N,
                         int K, int group_size, void* ws, size_t ws_bytes, hipStream_t stream);
+int launch_w4a16_qkv_rope(const void* act, const void* w, const void* scale, const void* cs, const void* sn,
+                          void* q_out, void* k_cache, void* v_cache, int M, int K, int group_size,
+                          int n_heads, int n_kv_heads, int max_len, int pos, void* ws, size_t ws_bytes,
+                          hipStream_t stream);
 int launch_w4a16(const void* act, const void* w, const void* scale, void* out, bool f32_out,
                  int M, int N, int K, int group_size, void* ws, size_t ws_bytes,
                  hipStream_t stream);

@@ -42,8 +42,18 @@ struct GemmParams {
     int wave_steps;      // streaming GEMV / 32x32 GEMM: 32-K steps per wave
     int m_tiles_;        // 32x32 GEMM: row tiles
     int vec_out;         // 32x32 GEMM: out is 16-byte aligned (vector stores)
-    int swiglu;          // streaming GEMV: SwiGLU epilogue (see store_swiglu)
+    // Streaming GEMV pair epilogues: each 64-column tile holds 32 column
+    // pairs (i, i + 32). kEpiSwiglu: see store_swiglu; kEpiQkvRope: see
+    // store_qkv_rope (rotary tables of the position, q output, KV cache).
+    int epilogue;
+    const uint16_t* rope_cos;   // [128]
+    const uint16_t* rope_sin;   // [128]
+    uint16_t* q_out;            // [M, n_q_heads, 128]
+    uint16_t* k_cache;          // [M, n_kv_heads, cache_len, 128]
+    uint16_t* v_cache;
+    int n_q_heads, n_kv_heads, cache_len, cache_pos;
 };
+constexpr int kEpiPlain = 0, kEpiSwiglu = 1, kEpiQkvRope = 2;
 
 // Eight int4 codes of one word -> four fp16 pairs, exact. Pair j holds the
 // codes of K positions (j, j + 4):
@@ -124,6 +134,37 @@ __device__ __forceinline__ void store_out(const GemmParams& p, int m, int n, flo
 __device__ __forceinline__ void store_swiglu(const GemmParams& p, int m, int c, float g, float u) {
     const float gh = h2f(f2h_bits(g)), uh = h2f(f2h_bits(u));
     static_cast<uint16_t*>(p.out)[(long)m * (p.N / 2) + c] = f2h_bits(silu_mul1(gh, uh));
+}
+
+// q|k|v epilogue of the streaming GEMV (head_dim 128). The weight's columns
+// are those of the concatenated q | k | v projection with each head's two
+// 64-dimension halves interleaved in 32-column blocks: tile t is head t / 2,
+// dimensions 32 (t % 2) .. + 31, then the same dimensions + 64, so pair i of
+// tile t is the rotary pair (d, d + 64), d = 32 (t % 2) + i. Both values are
+// rounded to fp16 (the fp16 q|k|v output) and stored as rope_qkv_append
+// stores them: q heads and k heads rotated (q to q_out, k into cache slot
+// cache_pos), v heads copied into their slot.
+__device__ __forceinline__ void store_qkv_rope(const GemmParams& p, int b, int tile, int i, float v1,
+                                               float v2) {
+    const int head = tile >> 1;
+    const int d = 32 * (tile & 1) + i;
+    const uint16_t h1 = f2h_bits(v1), h2 = f2h_bits(v2);
+    const int H = p.n_q_heads, Hkv = p.n_kv_heads;
+    if (head >= H + Hkv) {
+        uint16_t* dst = p.v_cache + (((long)b * Hkv + (head - H - Hkv)) * p.cache_len + p.cache_pos) * 128;
+        dst[d] = h1;
+        dst[d + 64] = h2;
+        return;
+    }
+    uint16_t* dst = head < H ? p.q_out + ((long)b * H + head) * 128
+                             : p.k_cache + (((long)b * Hkv + (head - H)) * p.cache_len + p.cache_pos) * 128;
+    rope_pair(h2f(h1), h2f(h2), h2f(p.rope_cos[d]), h2f(p.rope_sin[d]), h2f(p.rope_cos[d + 64]),
+              h2f(p.rope_sin[d + 64]), dst[d], dst[d + 64]);
+}
+
+__device__ __forceinline__ void store_pair(const GemmParams& p, int m, int tile, int i, float a, float b) {
+    if (p.epilogue == kEpiSwiglu) store_swiglu(p, m, tile * 32 + i, a, b);
+    else store_qkv_rope(p, m, tile, i, a, b);
 }
 
 // 4 consecutive outputs of row m from column n (a multiple of 4): one 16- /
@@ -773,10 +814,10 @@ __global__ __launch_bounds__(kStreamMaxWaves * kWave) void w4a16_gemv_stream_ker
     constexpr int TH = TN / 2;
     const int nhalf = min(p.M, MR) * TH;   // SwiGLU outputs of the tile
     if (p.splits == 1) {
-        if (p.swiglu) {
+        if (p.epilogue != kEpiPlain) {
             for (int o = t; o < nhalf; o += nthreads) {
                 const int row = o / TH, j = o % TH;
-                store_swiglu(p, row, n0 / 2 + j, tile_sum(row * TN + j), tile_sum(row * TN + TH + j));
+                store_pair(p, row, tile, j, tile_sum(row * TN + j), tile_sum(row * TN + TH + j));
             }
         } else {
             for (int o = t; o < nout; o += nthreads) store_out(p, o / TN, n0 + o % TN, tile_sum(o));
@@ -790,12 +831,12 @@ __global__ __launch_bounds__(kStreamMaxWaves * kWave) void w4a16_gemv_stream_ker
     if (t == 0) s_last = arrive_last(&p.counters[tile], (uint32_t)p.splits) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
-    if (p.swiglu) {
+    if (p.epilogue != kEpiPlain) {
         for (int o = t; o < nhalf; o += nthreads) {
             const int row = o / TH, j = o % TH;
             const float* base = p.part + (long)row * p.N + n0;
-            store_swiglu(p, row, n0 / 2 + j, sum_splits(base + j, (long)p.M * p.N, p.splits),
-                         sum_splits(base + TH + j, (long)p.M * p.N, p.splits));
+            store_pair(p, row, tile, j, sum_splits(base + j, (long)p.M * p.N, p.splits),
+                       sum_splits(base + TH + j, (long)p.M * p.N, p.splits));
         }
     } else {
         for (int o = t; o < nout; o += nthreads) {
@@ -1997,15 +2038,17 @@ GemmPlan plan_w4a16(int M, int N, int K, int group_size) {
     return plan_w4a16_mode(M, N, K, group_size, stream_override());
 }
 
-// The SwiGLU form always runs the streaming GEMV (its epilogue pairs the two
-// 32-column halves of each 64-column tile), so it needs that kernel's shape.
+// The pair epilogues (SwiGLU, q|k|v rope) always run the streaming GEMV (they
+// pair the two 32-column halves of each 64-column tile), so they need that
+// kernel's shape.
+static_assert(kStreamTile == 64, "the pair epilogues assume 64-column tiles");
 static bool swiglu_shape_ok(int M, int N, int K, int group_size) {
     const bool pow2_group = group_size >= 32 && (group_size & (group_size - 1)) == 0;
     return M >= 1 && M <= 16 && N > 0 && N % 64 == 0 && K > 0 && K % 32 == 0 && pow2_group &&
            (long)(K / 8) * N * 4 < (1L << 31) && (long)M * K * 2 < (1L << 31);
 }
 
-GemmPlan plan_w4a16_swiglu(int M, int N, int K, int group_size) {
+GemmPlan plan_w4a16_stream_forced(int M, int N, int K, int group_size) {
     if (!swiglu_shape_ok(M, N, K, group_size)) return GemmPlan{};
     return plan_w4a16_mode(M, N, K, group_size, 1);
 }
@@ -2038,12 +2081,42 @@ int launch_w4a16_swiglu(const void* act, const void* w, const void* scale, void*
         return set_error(LLMIK_ERR_UNSUPPORTED,
                          "w4a16 SwiGLU needs 1 <= M <= 16, N % 64 == 0, K % 32 == 0 and a power-of-two "
                          "group_size >= 32");
-    const GemmPlan pl = plan_w4a16_swiglu(M, N, K, group_size);
+    const GemmPlan pl = plan_w4a16_stream_forced(M, N, K, group_size);
     if (pl.kind != 5) return set_error(LLMIK_ERR_UNSUPPORTED, "w4a16 SwiGLU: no streaming plan");
     if (pl.splits > 1 && ws_bytes < pl.workspace_bytes)
         return set_error(LLMIK_ERR_WORKSPACE, "workspace too small for this W4A16 call");
     GemmParams p = gemm_params(pl, act, w, scale, out, false, M, N, K, group_size, ws);
-    p.swiglu = 1;
+    p.epilogue = kEpiSwiglu;
+    const int grid = pl.n_tiles * pl.splits;
+    if (M == 1) launch_stream<1>(p, grid, stream);
+    else launch_stream<16>(p, grid, stream);
+    return check_launch();
+}
+
+int launch_w4a16_qkv_rope(const void* act, const void* w, const void* scale, const void* cs, const void* sn,
+                          void* q_out, void* k_cache, void* v_cache, int M, int K, int group_size,
+                          int n_heads, int n_kv_heads, int max_len, int pos, void* ws, size_t ws_bytes,
+                          hipStream_t stream) {
+    const int N = (n_heads + 2 * n_kv_heads) * 128;
+    if (!swiglu_shape_ok(M, N, K, group_size))
+        return set_error(LLMIK_ERR_UNSUPPORTED,
+                         "w4a16 q|k|v rope needs 1 <= M <= 16, K % 32 == 0 and a power-of-two "
+                         "group_size >= 32");
+    const GemmPlan pl = plan_w4a16_stream_forced(M, N, K, group_size);
+    if (pl.kind != 5) return set_error(LLMIK_ERR_UNSUPPORTED, "w4a16 q|k|v rope: no streaming plan");
+    if (pl.splits > 1 && ws_bytes < pl.workspace_bytes)
+        return set_error(LLMIK_ERR_WORKSPACE, "workspace too small for this W4A16 call");
+    GemmParams p = gemm_params(pl, act, w, scale, nullptr, false, M, N, K, group_size, ws);
+    p.epilogue = kEpiQkvRope;
+    p.rope_cos = static_cast<const uint16_t*>(cs);
+    p.rope_sin = static_cast<const uint16_t*>(sn);
+    p.q_out = static_cast<uint16_t*>(q_out);
+    p.k_cache = static_cast<uint16_t*>(k_cache);
+    p.v_cache = static_cast<uint16_t*>(v_cache);
+    p.n_q_heads = n_heads;
+    p.n_kv_heads = n_kv_heads;
+    p.cache_len = max_len;
+    p.cache_pos = pos;
     const int grid = pl.n_tiles * pl.splits;
     if (M == 1) launch_stream<1>(p, grid, stream);
     else launch_stream<16>(p, grid, stream);

@@ -347,6 +347,44 @@ Tensor w4a16_gemm(const Tensor& act, const Tensor& weight_packed, const Tensor& 
     return gemm(act, weight_packed, scale, group_size, false);
 }
 
+Tensor w4a16_gemm_qkv_rope(const Tensor& act, const Tensor& weight_packed, const Tensor& scale, const Tensor& cos,
+                          const Tensor& sin, const Tensor& k_cache, const Tensor& v_cache, int64_t pos,
+                          int64_t n_heads, int64_t group_size) {
+    TORCH_CHECK(act.scalar_type() == at::kHalf && scale.scalar_type() == at::kHalf && cos.scalar_type() == at::kHalf &&
+                    sin.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
+                    v_cache.scalar_type() == at::kHalf,
+                "act, scale, cos, sin and the caches must be fp16");
+    TORCH_CHECK(weight_packed.scalar_type() == at::kInt, "weight_packed must be int32 (uint32 bit pattern)");
+    TORCH_CHECK(act.is_contiguous() && weight_packed.is_contiguous() && scale.is_contiguous() && cos.is_contiguous() &&
+                    sin.is_contiguous() && k_cache.is_contiguous() && v_cache.is_contiguous(),
+                "all tensors must be contiguous");
+    TORCH_CHECK(act.dim() == 2 && weight_packed.dim() == 2 && scale.dim() == 2, "act and weights must be 2D");
+    TORCH_CHECK(k_cache.dim() == 4 && k_cache.size(3) == 128 && v_cache.sizes() == k_cache.sizes(),
+                "k_cache and v_cache must be [batch, n_kv_heads, max_len, 128] of one shape");
+    TORCH_CHECK(cos.numel() == 128 && sin.numel() == 128, "cos and sin must be the position's 128 values");
+    const int M = act.size(0), K = act.size(1);
+    const int Hkv = k_cache.size(1), max_len = k_cache.size(2);
+    TORCH_CHECK(k_cache.size(0) == M, "the caches' batch must equal act's rows");
+    TORCH_CHECK(n_heads > 0 && n_heads % Hkv == 0, "n_heads must be a positive multiple of n_kv_heads");
+    const int N = (n_heads + 2 * Hkv) * 128;
+    TORCH_CHECK(weight_packed.size(1) == N && scale.size(1) == N, "weight N must be (n_heads + 2 n_kv_heads) * 128");
+    TORCH_CHECK(K == weight_packed.size(0) * 8, "act.K must equal weight_packed.K_packs * 8");
+    TORCH_CHECK(group_size > 0 && group_size % 8 == 0 && K == scale.size(0) * group_size,
+                "K must equal n_groups * group_size");
+    TORCH_CHECK(pos >= 0 && pos < max_len, "pos outside the cache");
+    TORCH_CHECK(act.is_cuda() && weight_packed.is_cuda() && scale.is_cuda() && cos.is_cuda() && sin.is_cuda() &&
+                    k_cache.is_cuda() && v_cache.is_cuda(), "all inputs must be CUDA tensors");
+    const c10::DeviceGuard guard(act.device());
+    Tensor q = at::empty({M, n_heads, 128}, act.options());
+    if (M == 0) return q;
+    const hipStream_t st = stream_of(act);
+    auto ws = workspace(act, st, llmik_w4a16_qkv_rope_workspace_size(M, (int)n_heads, Hkv, K, (int)group_size));
+    check(llmik_w4a16_gemm_qkv_rope_f16(ptr(act), ptr(weight_packed), ptr(scale), ptr(cos), ptr(sin), ptr(q),
+                                        ptr(k_cache), ptr(v_cache), M, K, (int)group_size, (int)n_heads, Hkv,
+                                        max_len, (int)pos, ws.first, ws.second, st));
+    return q;
+}
+
 Tensor w4a16_gemm_swiglu(const Tensor& act, const Tensor& weight_packed, const Tensor& scale, int64_t group_size) {
     TORCH_CHECK(act.scalar_type() == at::kHalf, "act must be fp16");
     TORCH_CHECK(weight_packed.scalar_type() == at::kInt, "weight_packed must be int32 (uint32 bit pattern)");
@@ -512,6 +550,7 @@ PYBIND11_MODULE(_C, m) {
     m.def("w4a16_gemm", &w4a16_gemm);
     m.def("w4a16_gemm_f32out", &w4a16_gemm_f32out);
     m.def("w4a16_gemm_swiglu", &w4a16_gemm_swiglu);
+    m.def("w4a16_gemm_qkv_rope", &w4a16_gemm_qkv_rope);
     m.def("w4a16_dequantize", &w4a16_dequantize);
     m.def("rmsnorm", &rmsnorm);
     m.def("silu_mul", &silu_mul);

@@ -48,7 +48,7 @@ __all__ = [
     "w4a16_gemm_f32out", "quantize_per_token_into", "quantize_v_per_token_int4_into",
     "quantize_k_per_channel_groupwise_int4_into", "quantize_weights_int4_groupwise",
     "pack_int4_along_k", "quantize_pack_weights_int4", "kivi_append_token_int4", "rope_qkv_append", "add_rmsnorm", "silu_mul_halves",
-    "w4a16_gemm_swiglu", "interleave_gate_up", "LIB_PATH",
+    "w4a16_gemm_swiglu", "interleave_gate_up", "w4a16_gemm_qkv_rope", "interleave_head_halves", "LIB_PATH",
 ]
 
 
@@ -276,6 +276,33 @@ def w4a16_gemm_swiglu(act: torch.Tensor, weight_packed: torch.Tensor, scale: tor
     _require(_is_device(act) and _is_device(weight_packed) and _is_device(scale),
              "all inputs must be CUDA tensors")
     return _C.w4a16_gemm_swiglu(act, weight_packed, scale, int(group_size))
+
+
+def interleave_head_halves(w: torch.Tensor) -> torch.Tensor:
+    """The column order `w4a16_gemm_qkv_rope` expects, from a concatenated
+    q | k | v weight [K, n_heads_total * 128]: each head's columns become
+    dimensions 0..31, 64..95, 32..63, 96..127 (its two halves interleaved in
+    32-column blocks). Quantising it column by column gives each column the
+    codes and scales it has in the concatenated weight."""
+    _require(w.dim() == 2 and w.shape[1] % 128 == 0, "w must be [K, n_heads_total * 128]")
+    K, n = w.shape
+    return w.reshape(K, n // 128, 2, 2, 32).transpose(2, 3).reshape(K, n)
+
+
+def w4a16_gemm_qkv_rope(act: torch.Tensor, weight_packed: torch.Tensor, scale: torch.Tensor,
+                        cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        pos: int, n_heads: int, group_size: int) -> torch.Tensor:
+    """The decode step's q|k|v projection, rope and cache append in one
+    launch (head_dim 128): returns the roped q [batch, n_heads, 128] and
+    writes slot `pos` of k_cache / v_cache [batch, n_kv_heads, max_len, 128],
+    for a weight whose columns are `interleave_head_halves(W_q | W_k | W_v)`
+    (prealloc_cache.py:42-110,132-133: the q/k/v projections, rope and the
+    cache update). The bits of `w4a16_gemm` on the concatenated weight and
+    `rope_qkv_append`. 1 <= batch <= 16."""
+    _require(all(_is_device(t) for t in (act, weight_packed, scale, cos, sin, k_cache, v_cache)),
+             "all inputs must be CUDA tensors")
+    return _C.w4a16_gemm_qkv_rope(act, weight_packed, scale, cos, sin, k_cache, v_cache, int(pos),
+                                  int(n_heads), int(group_size))
 
 
 def w4a16_dequantize(weight_packed: torch.Tensor, scale: torch.Tensor,

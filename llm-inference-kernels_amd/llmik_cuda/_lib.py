@@ -53,6 +53,9 @@ _SIGNATURES = {
     "llmik_w4a16_set_plan_override": (None, [_i, _i]),
     "llmik_w4a16_swiglu_workspace_size": (_sz, [_i, _i, _i, _i]),
     "llmik_w4a16_gemm_swiglu": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
+    "llmik_w4a16_qkv_rope_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
+    "llmik_w4a16_gemm_qkv_rope_f16": (
+        _i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "llmik_quantize_weights_int4_groupwise": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _p, _p]),
     "llmik_pack_int4_along_k": (_i, [_p, _i, _i, _p, _p]),
     "llmik_rmsnorm": (_i, [_p, _p, _p, _i, _i, _f, _p]),

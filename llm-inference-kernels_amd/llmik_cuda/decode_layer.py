@@ -13,14 +13,16 @@ projections are W4A16 `QuantizedLinear`s (integration/w4a16_patch.py:67-116).
     h = x + o_proj(decode_attention(q, kbuf, vbuf, scale, pos + 1))
     out = h + down_proj(silu_mul(gate_proj(n2), up_proj(n2))),  n2 = rmsnorm(h)
 
-With `fused=True` (the default) the step makes 9 launches instead of 17:
-q|k|v is one W4A16 projection over column-concatenated weights (codes and
-scales per column are those of the separate matrices), `rope_qkv_append`
-ropes q and k and writes the cache slot, `add_rmsnorm` takes the residual add
-and the second norm, and gate|up with its SwiGLU is one launch
-(`w4a16_gemm_swiglu` over the gate and up columns interleaved in 64-column
-tiles; batches above 16 rows keep the concatenated gate|up projection and
-`silu_mul_halves`). `fused=False` runs the op-by-op sequence above.
+With `fused=True` (the default) the step makes 8 launches instead of 17:
+the q|k|v projection, rope of q and k and the cache-slot writes are one
+launch (`w4a16_gemm_qkv_rope` over the concatenated weight with each head's
+halves interleaved), `add_rmsnorm` takes the residual add and the second
+norm, and gate|up with its SwiGLU is one launch (`w4a16_gemm_swiglu` over the
+gate and up columns interleaved in 64-column tiles). Codes and scales per
+column are those of the separate matrices. Where those launches do not apply
+(a batch above 16, another head_dim) the step runs a column-concatenated
+projection followed by `rope_qkv_append` / `silu_mul_halves`. `fused=False`
+runs the op-by-op sequence above.
 `DecodeStack` runs merged layers in sequence with each layer's last residual
 add carried into the next layer's first RMSNorm launch.
 
@@ -38,8 +40,9 @@ from typing import Dict, Optional, Tuple
 
 import torch
 
-from . import (add_rmsnorm, decode_attention, interleave_gate_up, quantize_pack_weights_int4, rmsnorm,
-               rope, rope_qkv_append, silu_mul, silu_mul_halves, w4a16_gemm, w4a16_gemm_swiglu)
+from . import (add_rmsnorm, decode_attention, interleave_gate_up, interleave_head_halves,
+               quantize_pack_weights_int4, rmsnorm, rope, rope_qkv_append, silu_mul, silu_mul_halves,
+               w4a16_gemm, w4a16_gemm_qkv_rope, w4a16_gemm_swiglu)
 
 
 class W4Linear:
@@ -59,6 +62,13 @@ class W4Linear:
     def swiglu(self, x: torch.Tensor) -> torch.Tensor:
         """silu(gate) * up of a weight built from `interleave_gate_up`."""
         return w4a16_gemm_swiglu(x, self.weight_packed, self.scale, self.group_size)
+
+    def qkv_rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, pos: int, n_heads: int) -> torch.Tensor:
+        """Roped q of a weight built from `interleave_head_halves`; k and v
+        into cache slot `pos`."""
+        return w4a16_gemm_qkv_rope(x, self.weight_packed, self.scale, cos, sin, k_cache, v_cache, pos,
+                                   n_heads, self.group_size)
 
 
 def rope_tables(max_len: int, head_dim: int, theta: float, device: torch.device) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -82,7 +92,8 @@ class DecodeLayer:
     (gate|up interleaved in 64-column tiles when the SwiGLU launch applies);
     `columns[name]` gives (key in `proj`, the indices of the columns of that
     projection's output, in order). `merge_swiglu=False` keeps the merged
-    step's gate|up projection and `silu_mul_halves` as two launches."""
+    step's gate|up projection and `silu_mul_halves` as two launches,
+    `merge_rope=False` its q|k|v projection and `rope_qkv_append`."""
 
     NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
@@ -90,7 +101,7 @@ class DecodeLayer:
                  max_len: int, device: Optional[torch.device] = None, head_dim: int = 128,
                  group_size: int = 128, eps: float = 1e-5, rope_theta: float = 500000.0,
                  weights: Optional[Dict[str, torch.Tensor]] = None, seed: int = 0,
-                 fused: bool = True, merge_swiglu: bool = True) -> None:
+                 fused: bool = True, merge_swiglu: bool = True, merge_rope: bool = True) -> None:
         if n_heads * head_dim != hidden or n_heads % n_kv_heads != 0:
             raise RuntimeError("hidden must be n_heads * head_dim and n_heads a multiple of n_kv_heads")
         dev = torch.device("cuda") if device is None else torch.device(device)
@@ -112,15 +123,26 @@ class DecodeLayer:
         # the merged kernels' limits: add_rmsnorm rows of at most 8192, 16-byte vectors
         self.fused = fused and hidden % 8 == 0 and hidden <= 8192 and intermediate % 8 == 0
         # gate|up + SwiGLU in one launch: the streaming GEMV's rows and tiles
-        self.swiglu = (self.fused and merge_swiglu and batch <= 16 and intermediate % 32 == 0
-                       and group_size >= 32 and group_size & (group_size - 1) == 0)
+        stream_ok = batch <= 16 and group_size >= 32 and group_size & (group_size - 1) == 0 and hidden % 32 == 0
+        self.swiglu = self.fused and merge_swiglu and stream_ok and intermediate % 32 == 0
+        # q|k|v + rope + cache append in one launch: the same, and 128-wide heads
+        self.qkv_rope = self.fused and merge_rope and stream_ok and head_dim == 128
         span = lambda a, b: torch.arange(a, b)  # noqa: E731
         if self.fused:
             cat = lambda *ns: torch.cat([weights.pop(n) for n in ns], dim=1)  # noqa: E731
-            self.proj = {"qkv": W4Linear(cat("q", "k", "v"), group_size), "o": W4Linear(weights.pop("o"), group_size),
+            qkv = cat("q", "k", "v")
+            n_qkv = hidden + 2 * kv
+            if self.qkv_rope:
+                qkv = interleave_head_halves(qkv)
+                c = span(0, n_qkv)
+                dd = c % 128
+                order = (c // 128) * 128 + (dd % 64 // 32) * 64 + (dd // 64) * 32 + dd % 32
+            else:
+                order = span(0, n_qkv)
+            self.proj = {"qkv": W4Linear(qkv, group_size), "o": W4Linear(weights.pop("o"), group_size),
                          "down": W4Linear(weights.pop("down"), group_size)}
-            self.columns = {"q": ("qkv", span(0, hidden)), "k": ("qkv", span(hidden, hidden + kv)),
-                            "v": ("qkv", span(hidden + kv, hidden + 2 * kv)), "o": ("o", span(0, hidden)),
+            self.columns = {"q": ("qkv", order[:hidden]), "k": ("qkv", order[hidden:hidden + kv]),
+                            "v": ("qkv", order[hidden + kv:]), "o": ("o", span(0, hidden)),
                             "down": ("down", span(0, hidden))}
             if self.swiglu:
                 self.proj["gate_up"] = W4Linear(interleave_gate_up(weights.pop("gate"), weights.pop("up")),
@@ -187,7 +209,10 @@ class DecodeLayer:
             n1 = rmsnorm(x, self.ln1, self.eps)
         else:
             x, n1 = add_rmsnorm(x, residual, self.ln1, self.eps)
-        q = rope_qkv_append(p["qkv"](n1), self.cos[pos], self.sin[pos], self.kbuf, self.vbuf, pos)
+        if self.qkv_rope:
+            q = p["qkv"].qkv_rope(n1, self.cos[pos], self.sin[pos], self.kbuf, self.vbuf, pos, H)
+        else:
+            q = rope_qkv_append(p["qkv"](n1), self.cos[pos], self.sin[pos], self.kbuf, self.vbuf, pos)
         attn = decode_attention(q, self.kbuf, self.vbuf, self.scale, pos + 1)
         h, n2 = add_rmsnorm(x, p["o"](attn.view(B, H * D)), self.ln2, self.eps)
         act = p["gate_up"].swiglu(n2) if self.swiglu else silu_mul_halves(p["gate_up"](n2))
@@ -204,8 +229,8 @@ class DecodeLayer:
 class DecodeStack:
     """Merged-step layers run in sequence for one token. Layer i's last
     residual add goes into layer i + 1's first RMSNorm launch
-    (`step_parts(..., residual=)`), so n layers make 8 n + 1 launches (9 n + 1
-    without the gate|up SwiGLU launch); the
+    (`step_parts(..., residual=)`), so n layers make 7 n + 1 launches (one
+    more per layer for each merged projection that does not apply); the
     output equals chaining `layer.step` bit for bit (the merged norm rounds
     x + residual exactly as the add it replaces)."""
 

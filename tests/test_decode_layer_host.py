@@ -62,3 +62,20 @@ def test_interleave_gate_up_tiles():
     assert torch.equal(w[:, cols], gate) and torch.equal(w[:, cols + 32], up)
     with pytest.raises(RuntimeError, match="I % 32"):
         llmik_cuda.interleave_gate_up(gate[:, :40], up[:, :40])
+
+
+def test_interleave_head_halves_pairs_rotary_dimensions():
+    """Each head's 128 columns become dimensions 0..31, 64..95, 32..63,
+    96..127: in 64-column tile t, column i pairs with i + 32 as the rotary
+    pair (d, d + 64), d = 32 (t % 2) + i."""
+    import llmik_cuda
+    K, heads = 2, 3
+    w = torch.arange(K * heads * 128, dtype=torch.float32).reshape(K, heads * 128)
+    wi = llmik_cuda.interleave_head_halves(w)
+    for t in range(2 * heads):
+        for i in range(32):
+            d = 32 * (t % 2) + i
+            assert torch.equal(wi[:, 64 * t + i], w[:, 128 * (t // 2) + d])
+            assert torch.equal(wi[:, 64 * t + 32 + i], w[:, 128 * (t // 2) + d + 64])
+    with pytest.raises(RuntimeError, match="n_heads_total"):
+        llmik_cuda.interleave_head_halves(w[:, :100])

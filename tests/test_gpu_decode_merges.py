@@ -1,6 +1,6 @@
 """GPU: the decode-step merges (rope_qkv_append, add_rmsnorm,
-silu_mul_halves, w4a16_gemm_swiglu) give the same bits as the ops they
-replace, which the fused op and W4A16 tests pin against the fp32 oracle;
+silu_mul_halves, w4a16_gemm_swiglu, w4a16_gemm_qkv_rope) give the same bits
+as the ops they replace, which the fused op and W4A16 tests pin against the fp32 oracle;
 add_rmsnorm and w4a16_gemm_swiglu are also checked against the oracle
 directly."""
 from __future__ import annotations
@@ -135,3 +135,51 @@ def test_w4a16_gemm_swiglu_rejects_unsupported_shapes(llmik, cuda):
         llmik.w4a16_gemm_swiglu(act, w, s, 128)
     with pytest.raises(RuntimeError, match="N % 64"):
         llmik.w4a16_gemm_swiglu(act[:4], w[:, :96].contiguous(), s[:, :96].contiguous(), 128)
+
+
+@pytest.mark.parametrize("B,K,H,Hkv,max_len,pos", [(8, 4096, 32, 8, 64, 17), (1, 4096, 32, 8, 8, 7),
+                                                   (16, 512, 4, 2, 40, 0), (3, 2048, 6, 3, 9, 4),
+                                                   (5, 256, 2, 1, 3, 2)])
+def test_w4a16_gemm_qkv_rope_equals_gemm_then_rope_qkv_append(llmik, cuda, B, K, H, Hkv, max_len, pos):
+    """q|k|v projection + rope + cache append in one launch over the
+    head-interleaved weight gives the bits of the q|k|v product over the
+    concatenated weight (on the same streaming GEMV plan) followed by
+    rope_qkv_append: the same q, the same slot `pos` of both caches, every
+    other slot untouched (shapes: the Llama-3-8B q|k|v at B = 8 and 1, K
+    splits, GQA 2 and 3, MHA-like 2:1, first and last slots)."""
+    from llmik_cuda._lib import lib
+    gen = torch.Generator(device=cuda).manual_seed(B * 7 + K + H + pos)
+    n = (H + 2 * Hkv) * 128
+    w = torch.randn((K, n), generator=gen, device=cuda) * 0.02
+    wc, sc_c = llmik.quantize_pack_weights_int4(w.contiguous(), 128)
+    wi, sc_i = llmik.quantize_pack_weights_int4(llmik.interleave_head_halves(w).contiguous(), 128)
+    act = torch.randn((B, K), generator=gen, device=cuda).half()
+    cos = torch.randn(128, generator=gen, device=cuda).half()
+    sin = torch.randn(128, generator=gen, device=cuda).half()
+    kc = torch.randn((B, Hkv, max_len, 128), generator=gen, device=cuda).half()
+    vc = torch.randn((B, Hkv, max_len, 128), generator=gen, device=cuda).half()
+    k_ref, v_ref = kc.clone(), vc.clone()
+    q = llmik.w4a16_gemm_qkv_rope(act, wi, sc_i, cos, sin, kc, vc, pos, H, 128)
+    assert q.shape == (B, H, 128) and q.dtype == torch.float16
+    lib.llmik_w4a16_set_plan_override(1, -1)   # the concatenated product on the streaming GEMV too
+    try:
+        qkv = llmik.w4a16_gemm(act, wc, sc_c, 128)
+    finally:
+        lib.llmik_w4a16_set_plan_override(-1, -1)
+    q_ref = llmik.rope_qkv_append(qkv, cos, sin, k_ref, v_ref, pos)
+    assert torch.equal(q, q_ref)
+    assert torch.equal(kc, k_ref) and torch.equal(vc, v_ref)
+
+
+def test_w4a16_gemm_qkv_rope_rejects_bad_arguments(llmik, cuda):
+    act = torch.zeros((17, 256), dtype=torch.float16, device=cuda)
+    w = torch.zeros((32, 4 * 128), dtype=torch.int32, device=cuda)
+    s = torch.ones((2, 4 * 128), dtype=torch.float16, device=cuda)
+    cs = torch.zeros(128, dtype=torch.float16, device=cuda)
+    kc = torch.zeros((17, 1, 4, 128), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="M <= 16"):
+        llmik.w4a16_gemm_qkv_rope(act, w, s, cs, cs, kc, kc.clone(), 1, 2, 128)
+    with pytest.raises(RuntimeError, match="pos outside the cache"):
+        llmik.w4a16_gemm_qkv_rope(act[:2], w, s, cs, cs, kc[:2].contiguous(), kc[:2].clone(), 4, 2, 128)
+    with pytest.raises(RuntimeError, match="n_heads \\+ 2 n_kv_heads"):
+        llmik.w4a16_gemm_qkv_rope(act[:2], w, s, cs, cs, kc[:2].contiguous(), kc[:2].clone(), 0, 4, 128)
