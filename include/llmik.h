@@ -295,9 +295,10 @@ LLMIK_API llmik_status llmik_w4a16_gemm_swiglu(const void* act, const void* weig
  * rows; q_out [batch, n_heads, 128] gets the roped q, slot `pos` of k_cache /
  * v_cache [batch, n_kv_heads, max_len, 128] the roped k and v. Needs
  * 1 <= batch <= 16, K % 32 == 0 and a power-of-two group_size >= 32
- * (LLMIK_ERR_UNSUPPORTED otherwise); workspace of
- * llmik_w4a16_qkv_rope_workspace_size(...) bytes, with the rules of
- * llmik_w4a16_gemm.
+ * (LLMIK_ERR_UNSUPPORTED otherwise), pos < max_len; the alignment rules of
+ * llmik_w4a16_gemm with q_out as its out, 2 bytes for cos, sin and the
+ * caches; workspace of llmik_w4a16_qkv_rope_workspace_size(...) bytes, with
+ * the rules of llmik_w4a16_gemm.
  */
 LLMIK_API size_t llmik_w4a16_qkv_rope_workspace_size(int batch, int n_heads, int n_kv_heads, int K,
                                                      int group_size);
