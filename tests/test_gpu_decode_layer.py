@@ -142,3 +142,23 @@ def test_stack_equals_chained_layer_steps(llmik, cuda):
         assert torch.equal(out, chained), f"replay {r}"
     with pytest.raises(RuntimeError, match="fused=True"):
         DecodeStack([_layer(cuda, seed=9, fused=False)])
+
+
+@pytest.mark.parametrize("batch,merge", [(20, True), (4, False)])
+def test_merged_step_without_the_projection_merges(llmik, cuda, batch, merge):
+    """The merged step where its two projection merges do not apply (a batch
+    above 16 rows) or are switched off: the concatenated q|k|v and gate|up
+    projections with rope_qkv_append and silu_mul_halves, against the same
+    oracle composition."""
+    from llmik_cuda.decode_layer import DecodeLayer
+    cfg = dict(CFG, batch=batch)
+    layer = DecodeLayer(device=cuda, seed=3, merge_swiglu=merge, merge_rope=merge, **cfg)
+    assert layer.fused and not layer.swiglu and not layer.qkv_rope
+    g = torch.Generator(device=cuda).manual_seed(103)
+    layer.kbuf[:, :, :POS] = torch.randn(layer.kbuf[:, :, :POS].shape, generator=g, device=cuda).half()
+    layer.vbuf[:, :, :POS] = torch.randn(layer.vbuf[:, :, :POS].shape, generator=g, device=cuda).half()
+    x = torch.randn((batch, CFG["hidden"]), generator=g, device=cuda).half()
+    k0, v0 = layer.kbuf.cpu().numpy(), layer.vbuf.cpu().numpy()
+    got = layer.step(x, POS).cpu().numpy().astype(np.float32)
+    ref = _oracle_step(layer, x.cpu().numpy(), k0, v0, POS).astype(np.float32)
+    assert np.abs(got - ref).max() <= 1e-2
