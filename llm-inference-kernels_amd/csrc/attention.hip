@@ -83,6 +83,70 @@ struct AttnParams {
 // Shared tail: merge NR partial states held in LDS, then either write the
 // output (single split) or publish the split and let the last one combine.
 // ---------------------------------------------------------------------------
+// The last split's combine of a (batch, kv head, head chunk) slot group:
+// each thread issues the (m, l) and partial-output loads of a batch of KB
+// splits for all of its outputs together, so a combine of up to KB splits
+// costs one memory round trip; rescaling to a common maximum is done in
+// registers. Batch entries past the split count re-read the last split and
+// add zero.
+template <int KB, int kPer, int HPW, int NT>
+__device__ __forceinline__ void combine_splits(const AttnParams& p, int b, int slot_group, int head0) {
+    const int tid = threadIdx.x;
+    constexpr int kOuts = HPW * kHeadDim;
+    const long base = (long)slot_group * p.n_splits;
+    float gm[kPer], so[kPer], sl[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        gm[i] = -INFINITY;
+        so[i] = 0.0f;
+        sl[i] = 0.0f;
+    }
+    for (int sp0 = 0; sp0 < p.n_splits; sp0 += KB) {
+        float mv[kPer][KB], lv[kPer][KB], ov[kPer][KB];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = min(tid + i * NT, kOuts - 1);
+            const int h = idx / kHeadDim, d = idx % kHeadDim;
+#pragma unroll
+            for (int u = 0; u < KB; ++u) {
+                const long sl_idx = (base + min(sp0 + u, p.n_splits - 1)) * HPW + h;
+                mv[i][u] = publish_load(&p.part_ml[sl_idx * 2]);
+                lv[i][u] = publish_load(&p.part_ml[sl_idx * 2 + 1]);
+                ov[i][u] = publish_load(&p.part_o[sl_idx * kHeadDim + d]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            float bm = gm[i];
+#pragma unroll
+            for (int u = 0; u < KB; ++u)
+                if (sp0 + u < p.n_splits) bm = fmaxf(bm, mv[i][u]);
+            if (bm == -INFINITY) continue;
+            const float r = (gm[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(gm[i] - bm);
+            so[i] *= r;
+            sl[i] *= r;
+#pragma unroll
+            for (int u = 0; u < KB; ++u) {
+                const float w = (sp0 + u < p.n_splits && mv[i][u] != -INFINITY)
+                                    ? __builtin_amdgcn_exp2f(mv[i][u] - bm) : 0.0f;
+                so[i] = fmaf(ov[i][u], w, so[i]);
+                sl[i] = fmaf(lv[i][u], w, sl[i]);
+            }
+            gm[i] = bm;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < kOuts) {
+            const int h = idx / kHeadDim, d = idx % kHeadDim;
+            const float inv = (sl[i] > 0.0f) ? 1.0f / sl[i] : 0.0f;
+            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so[i] * inv);
+        }
+    }
+}
+
+
 template <int NR, int HPW, int NT>
 __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*s_o)[HPW][kHeadDim],
                                              const float (*s_m)[HPW], const float (*s_l)[HPW],
@@ -152,63 +216,14 @@ __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*
     __syncthreads();
     if (*s_last == 0u) return;
 
-    // Last split of this (batch, kv head, head chunk): combine all splits.
-    // Each thread issues the (m, l) and partial-output loads of a batch of
-    // splits for all of its outputs together, so a combine of up to kBatch
-    // splits costs one memory round trip; rescaling to a common maximum is
-    // done in registers.
-    constexpr int kBatch = (kPer == 1) ? 16 : 8;
-    const long base = (long)slot_group * p.n_splits;
-    float gm[kPer], so[kPer], sl[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        gm[i] = -INFINITY;
-        so[i] = 0.0f;
-        sl[i] = 0.0f;
-    }
-    for (int sp0 = 0; sp0 < p.n_splits; sp0 += kBatch) {
-        float mv[kPer][kBatch], lv[kPer][kBatch], ov[kPer][kBatch];
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int idx = min(tid + i * NT, kOuts - 1);
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const long sl_idx = (base + min(sp0 + u, p.n_splits - 1)) * HPW + h;
-                mv[i][u] = publish_load(&p.part_ml[sl_idx * 2]);
-                lv[i][u] = publish_load(&p.part_ml[sl_idx * 2 + 1]);
-                ov[i][u] = publish_load(&p.part_o[sl_idx * kHeadDim + d]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            float bm = gm[i];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                if (sp0 + u < p.n_splits) bm = fmaxf(bm, mv[i][u]);
-            if (bm == -INFINITY) continue;
-            const float r = (gm[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(gm[i] - bm);
-            so[i] *= r;
-            sl[i] *= r;
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const float w = (sp0 + u < p.n_splits && mv[i][u] != -INFINITY)
-                                    ? __builtin_amdgcn_exp2f(mv[i][u] - bm) : 0.0f;
-                so[i] = fmaf(ov[i][u], w, so[i]);
-                sl[i] = fmaf(lv[i][u], w, sl[i]);
-            }
-            gm[i] = bm;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < kOuts) {
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-            const float inv = (sl[i] > 0.0f) ? 1.0f / sl[i] : 0.0f;
-            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so[i] * inv);
-        }
-    }
+    // Last split of this slot group: combine all splits, in batches of the
+    // split count rounded up to 4, 8 or 16 (at most 8 with two outputs per
+    // thread), so that a combine of 4 splits issues 4 loads per value and
+    // not 16. The batches run in split order, so the sum is the same bits
+    // for every batch size.
+    if (p.n_splits <= 4) combine_splits<4, kPer, HPW, NT>(p, b, slot_group, head0);
+    else if (p.n_splits <= 8 || kPer > 1) combine_splits<8, kPer, HPW, NT>(p, b, slot_group, head0);
+    else combine_splits<16, kPer, HPW, NT>(p, b, slot_group, head0);
     if (tid == 0) p.counters[slot_group] = 0u;   // leave the counter zeroed for the next call
 }
 
