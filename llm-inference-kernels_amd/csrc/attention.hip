@@ -79,135 +79,119 @@ struct AttnParams {
     float scale_log2;
 };
 
+// Split hand-off. Thread t < HPW * 32 of the workgroup owns head t / 32,
+// channels 4 (t % 32) .. + 3 of the workgroup's outputs; the partials and
+// the combine move those four values as one 16-byte access (sc1, like the
+// 4-byte forms above), and the output as one 8-byte store.
+template <int HPW>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_o_rsrc(const AttnParams& p, long slot) {
+    return make_buffer_rsrc(p.part_o + slot * HPW * kHeadDim, (uint32_t)(HPW * kHeadDim * sizeof(float)));
+}
+
+__device__ __forceinline__ void store_out4_f16(const AttnParams& p, long o, const float v[4], float inv) {
+    const uint32_t lo = (uint32_t)f2h_bits(v[0] * inv) | ((uint32_t)f2h_bits(v[1] * inv) << 16);
+    const uint32_t hi = (uint32_t)f2h_bits(v[2] * inv) | ((uint32_t)f2h_bits(v[3] * inv) << 16);
+    *reinterpret_cast<u32x2*>(p.out + o) = u32x2{lo, hi};
+}
+
+// The last split's combine of a (batch, kv head, head chunk) slot group: each
+// thread issues the (m, l) and partial-output loads of a batch of KB splits
+// together, so a combine of up to KB splits costs one memory round trip;
+// rescaling to a common maximum is done in registers. Batch entries past the
+// split count re-read the last split and add zero.
+template <int KB, int HPW>
+__device__ __forceinline__ void combine_splits(const AttnParams& p, int b, int slot_group, int head0, int h,
+                                               int d) {
+    const long base = (long)slot_group * p.n_splits;
+    float gm = -INFINITY, sl = 0.0f;
+    float so[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sp0 = 0; sp0 < p.n_splits; sp0 += KB) {
+        float mv[KB], lv[KB];
+        u32x4 ov[KB];
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const long slot = base + min(sp0 + u, p.n_splits - 1);
+            mv[u] = publish_load(&p.part_ml[(slot * HPW + h) * 2]);
+            lv[u] = publish_load(&p.part_ml[(slot * HPW + h) * 2 + 1]);
+            ov[u] = publish_load16(part_o_rsrc<HPW>(p, slot), (uint32_t)((h * kHeadDim + d) * sizeof(float)));
+        }
+        float bm = gm;
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (sp0 + u < p.n_splits) bm = fmaxf(bm, mv[u]);
+        if (bm == -INFINITY) continue;
+        const float r = (gm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(gm - bm);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) so[e] *= r;
+        sl *= r;
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const float w = (sp0 + u < p.n_splits && mv[u] != -INFINITY) ? __builtin_amdgcn_exp2f(mv[u] - bm)
+                                                                         : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t ob = ov[u][e];
+                so[e] = fmaf(__uint_as_float(ob), w, so[e]);
+            }
+            sl = fmaf(lv[u], w, sl);
+        }
+        gm = bm;
+    }
+    const float inv = (sl > 0.0f) ? 1.0f / sl : 0.0f;
+    store_out4_f16(p, ((long)b * p.n_heads + head0 + h) * kHeadDim + d, so, inv);
+}
+
 // ---------------------------------------------------------------------------
 // Shared tail: merge NR partial states held in LDS, then either write the
 // output (single split) or publish the split and let the last one combine.
 // ---------------------------------------------------------------------------
-// The last split's combine of a (batch, kv head, head chunk) slot group:
-// each thread issues the (m, l) and partial-output loads of a batch of KB
-// splits for all of its outputs together, so a combine of up to KB splits
-// costs one memory round trip; rescaling to a common maximum is done in
-// registers. Batch entries past the split count re-read the last split and
-// add zero.
-template <int KB, int kPer, int HPW, int NT>
-__device__ __forceinline__ void combine_splits(const AttnParams& p, int b, int slot_group, int head0) {
-    const int tid = threadIdx.x;
-    constexpr int kOuts = HPW * kHeadDim;
-    const long base = (long)slot_group * p.n_splits;
-    float gm[kPer], so[kPer], sl[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        gm[i] = -INFINITY;
-        so[i] = 0.0f;
-        sl[i] = 0.0f;
-    }
-    for (int sp0 = 0; sp0 < p.n_splits; sp0 += KB) {
-        float mv[kPer][KB], lv[kPer][KB], ov[kPer][KB];
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int idx = min(tid + i * NT, kOuts - 1);
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-#pragma unroll
-            for (int u = 0; u < KB; ++u) {
-                const long sl_idx = (base + min(sp0 + u, p.n_splits - 1)) * HPW + h;
-                mv[i][u] = publish_load(&p.part_ml[sl_idx * 2]);
-                lv[i][u] = publish_load(&p.part_ml[sl_idx * 2 + 1]);
-                ov[i][u] = publish_load(&p.part_o[sl_idx * kHeadDim + d]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            float bm = gm[i];
-#pragma unroll
-            for (int u = 0; u < KB; ++u)
-                if (sp0 + u < p.n_splits) bm = fmaxf(bm, mv[i][u]);
-            if (bm == -INFINITY) continue;
-            const float r = (gm[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(gm[i] - bm);
-            so[i] *= r;
-            sl[i] *= r;
-#pragma unroll
-            for (int u = 0; u < KB; ++u) {
-                const float w = (sp0 + u < p.n_splits && mv[i][u] != -INFINITY)
-                                    ? __builtin_amdgcn_exp2f(mv[i][u] - bm) : 0.0f;
-                so[i] = fmaf(ov[i][u], w, so[i]);
-                sl[i] = fmaf(lv[i][u], w, sl[i]);
-            }
-            gm[i] = bm;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < kOuts) {
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-            const float inv = (sl[i] > 0.0f) ? 1.0f / sl[i] : 0.0f;
-            p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(so[i] * inv);
-        }
-    }
-}
-
-
 template <int NR, int HPW, int NT>
 __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*s_o)[HPW][kHeadDim],
                                              const float (*s_m)[HPW], const float (*s_l)[HPW],
                                              uint32_t* s_last, int b, int kvh, int hchunk,
                                              int split, int head0) {
+    constexpr int kThr = HPW * (kHeadDim / 4);   // threads owning four outputs
+    static_assert(NT >= kThr, "the workgroup must cover every output");
     const int tid = threadIdx.x;
-    constexpr int kOuts = HPW * kHeadDim;
-    constexpr int kPer = (kOuts + NT - 1) / NT;
+    const bool owner = tid < kThr;
+    const int h = owner ? tid / (kHeadDim / 4) : 0;
+    const int d = owner ? 4 * (tid % (kHeadDim / 4)) : 0;
     const int slot_group = (b * p.n_kv_heads + kvh) * p.n_hchunks + hchunk;
     const long slot = (long)slot_group * p.n_splits + split;
-    float wo[kPer], wm[kPer], wl[kPer];
+    float wo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float wm = -INFINITY, wl = 0.0f;
+    if (owner) {
+        float gm = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int idx = tid + i * NT;
-        wo[i] = 0.0f;
-        wm[i] = -INFINITY;
-        wl[i] = 0.0f;
-        if (idx < kOuts) {
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-            float gm = -INFINITY;
+        for (int r = 0; r < NR; ++r) gm = fmaxf(gm, s_m[r][h]);
+        if (gm != -INFINITY) {
 #pragma unroll
-            for (int r = 0; r < NR; ++r) gm = fmaxf(gm, s_m[r][h]);
-            float so = 0.0f, sl = 0.0f;
-            if (gm != -INFINITY) {
+            for (int r = 0; r < NR; ++r) {
+                const float w = (s_m[r][h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_m[r][h] - gm);
+                const f32x4 o4 = *reinterpret_cast<const f32x4*>(&s_o[r][h][d]);
 #pragma unroll
-                for (int r = 0; r < NR; ++r) {
-                    const float w = (s_m[r][h] == -INFINITY) ? 0.0f
-                                                              : __builtin_amdgcn_exp2f(s_m[r][h] - gm);
-                    so = fmaf(s_o[r][h][d], w, so);
-                    sl = fmaf(s_l[r][h], w, sl);
-                }
+                for (int e = 0; e < 4; ++e) wo[e] = fmaf(o4[e], w, wo[e]);
+                wl = fmaf(s_l[r][h], w, wl);
             }
-            wo[i] = so;
-            wm[i] = gm;
-            wl[i] = sl;
         }
+        wm = gm;
     }
 
     if (p.n_splits == 1) {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int idx = tid + i * NT;
-            if (idx < kOuts) {
-                const int h = idx / kHeadDim, d = idx % kHeadDim;
-                const float inv = (wl[i] > 0.0f) ? 1.0f / wl[i] : 0.0f;
-                p.out[((long)b * p.n_heads + head0 + h) * kHeadDim + d] = f2h_bits(wo[i] * inv);
-            }
+        if (owner) {
+            const float inv = (wl > 0.0f) ? 1.0f / wl : 0.0f;
+            store_out4_f16(p, ((long)b * p.n_heads + head0 + h) * kHeadDim + d, wo, inv);
         }
         return;
     }
 
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < kOuts) {
-            const int h = idx / kHeadDim, d = idx % kHeadDim;
-            publish_store(&p.part_o[(slot * HPW + h) * kHeadDim + d], wo[i]);
-            if (d == 0) {
-                publish_store(&p.part_ml[(slot * HPW + h) * 2 + 0], wm[i]);
-                publish_store(&p.part_ml[(slot * HPW + h) * 2 + 1], wl[i]);
-            }
+    if (owner) {
+        publish_store16(part_o_rsrc<HPW>(p, slot), (uint32_t)((h * kHeadDim + d) * sizeof(float)),
+                        make_u32x4(__float_as_uint(wo[0]), __float_as_uint(wo[1]), __float_as_uint(wo[2]),
+                                   __float_as_uint(wo[3])));
+        if (d == 0) {
+            publish_store(&p.part_ml[(slot * HPW + h) * 2 + 0], wm);
+            publish_store(&p.part_ml[(slot * HPW + h) * 2 + 1], wl);
         }
     }
     publish_wait();
@@ -217,13 +201,14 @@ __device__ __forceinline__ void finish_split(const AttnParams& p, const float (*
     if (*s_last == 0u) return;
 
     // Last split of this slot group: combine all splits, in batches of the
-    // split count rounded up to 4, 8 or 16 (at most 8 with two outputs per
-    // thread), so that a combine of 4 splits issues 4 loads per value and
-    // not 16. The batches run in split order, so the sum is the same bits
-    // for every batch size.
-    if (p.n_splits <= 4) combine_splits<4, kPer, HPW, NT>(p, b, slot_group, head0);
-    else if (p.n_splits <= 8 || kPer > 1) combine_splits<8, kPer, HPW, NT>(p, b, slot_group, head0);
-    else combine_splits<16, kPer, HPW, NT>(p, b, slot_group, head0);
+    // split count rounded up to 4, 8 or 16, so that a combine of 4 splits
+    // issues 4 loads per value and not 16. The batches run in split order,
+    // so the sum is the same bits for every batch size.
+    if (owner) {
+        if (p.n_splits <= 4) combine_splits<4, HPW>(p, b, slot_group, head0, h, d);
+        else if (p.n_splits <= 8) combine_splits<8, HPW>(p, b, slot_group, head0, h, d);
+        else combine_splits<16, HPW>(p, b, slot_group, head0, h, d);
+    }
     if (tid == 0) p.counters[slot_group] = 0u;   // leave the counter zeroed for the next call
 }
 
@@ -731,7 +716,7 @@ void decode_attention_mfma_kernel(AttnParams p) {
     // ---- merge the wave states through LDS ----
     const float l_tot = row16_sum(l_run);   // lane group g: head g's denominator
 
-    __shared__ float s_o[NW][HPW][kHeadDim];
+    __shared__ __attribute__((aligned(16))) float s_o[NW][HPW][kHeadDim];
     __shared__ float s_m[NW][HPW];
     __shared__ float s_l[NW][HPW];
     __shared__ uint32_t s_last;
@@ -937,7 +922,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_valu_kernel(Att
         }
     }
 
-    __shared__ float s_o[kRows][HPW][kHeadDim];
+    __shared__ __attribute__((aligned(16))) float s_o[kRows][HPW][kHeadDim];
     __shared__ float s_m[kRows][HPW];
     __shared__ float s_l[kRows][HPW];
     __shared__ uint32_t s_last;
@@ -977,7 +962,7 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
     const int cus = device_cu_count();
     // Aim for kAttnWgsPerCu workgroups per CU. Calls that must split the
     // sequence to fill the chip use 8-wave workgroups (more loads in flight
-    // per CU, one combine output per thread); otherwise 4 waves. Every split
+    // per CU); otherwise 4 waves. Every split
     // gets at least one 32-token tile per wave.
     // A short sequence that 8-wave splits (one 256-token step each) cannot
     // spread over the chip runs 4-wave splits instead, as long as that keeps
