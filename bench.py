@@ -19,6 +19,16 @@ Method
   * The K timed steps are captured in one HIP graph on a dedicated stream and
     replayed once; HIP events recorded on that stream bracket the replay,
     with torch.cuda.synchronize() on both sides. Per-launch time = elapsed/K.
+  * Untimed warm-up before it: one eager call per input set, then replays of
+    the same graph, at least W calls (--warmup, default 16000) and at least
+    0.4 s of GPU time, then one settling replay: after the host-side set-up
+    the kernels run a few per cent slower until the GPU has been under
+    sustained load for 17-140 ms ("warmup_calls" in the output counts the
+    untimed calls).
+  * Each attention and W4A16 row also carries "dist": the median, p10 and
+    p90 per-call time over 100 replays (after 25 warm-up replays) of a graph
+    of max(20, sets) calls over the input sets, each replay bracketed by its
+    own events.
   * Before timing, every config is checked against a float64 torch
     computation on the GPU (max-abs 2e-3); a failing config aborts the run.
   * roofline.achieved = algorithmic bytes per launch / per-launch time, with
@@ -78,18 +88,35 @@ def w4a16_bytes(M: int, K: int, N: int, gs: int = 128) -> int:
 
 # ----------------------------------------------------------------- timing
 
-def time_steps(steps_fns, warmup: int, reps: int, all_sets: bool = True):
-    """Warm up eagerly, capture `reps` steps (cycling through steps_fns) in a
-    HIP graph and time one replay with events on the capture stream.
-    With `all_sets`, the graph holds at least one step per input set, so a
-    replay reads every set. Returns per-step microseconds."""
+WARM_MS = 400.0   # untimed replays before a timed one: at least this much GPU time
+
+
+def time_steps(steps_fns, warmup: int, reps: int, all_sets: bool = True, info: dict | None = None):
+    """Capture `reps` steps (cycling through steps_fns) in a HIP graph, warm
+    up, and time one replay with events on the capture stream.
+
+    Untimed warm-up: one eager call per input set (an op's per-stream
+    workspace is allocated and zeroed on its first call, which must not land
+    inside the graph), then replays of the same graph, ceil(warmup / reps)
+    of them and at least WARM_MS of GPU time. After the host-side set-up
+    between configs the kernels run a few per cent slower until the GPU has
+    been under sustained load for a while, then step down and stay there
+    (kernel traces: fp16 B=64 S=8192 322-324 -> 308-309 us per call 48 ms
+    into the run, S=32768 166-168 -> 158-160 us after 140 ms, INT8 A8
+    15.7 -> 14.9 us after 17 ms; at A16, after 200 ms idle, one or two warm
+    replays left 25.5-26.1 us, five or more 25.3-25.4). WARM_MS covers the
+    slowest switch seen; one more untimed replay after the burst settles the
+    runtime (below). With `all_sets`, the graph holds at least one step
+    per input set, so a replay reads every set. Returns per-step
+    microseconds; `info`, if given, receives the untimed call count as
+    "warmup_calls"."""
     import torch
     if all_sets:
         reps = max(reps, len(steps_fns))
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        for i in range(max(warmup, len(steps_fns))):
-            steps_fns[i % len(steps_fns)]()
+        for fn in steps_fns:
+            fn()
     stream.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
@@ -98,15 +125,70 @@ def time_steps(steps_fns, warmup: int, reps: int, all_sets: bool = True):
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):   # replay() launches on the current stream
-        graph.replay()                # one untimed replay (page-in of the graph itself)
+        start.record(stream)
+        graph.replay()                # first untimed replay: its length sizes the warm-up
+        end.record(stream)
+        torch.cuda.synchronize()
+        n_warm = max(-(-warmup // reps), math.ceil(WARM_MS / max(start.elapsed_time(end), 1e-3)))
+        n_warm = min(n_warm, 4000)
+        for _ in range(n_warm - 1):
+            graph.replay()
+        torch.cuda.synchronize()
+        # The first replay after a burst of hundreds pays a one-off runtime
+        # cost (measured: after 400-800 queued replays of a 50-call graph
+        # the next replay took 15.8-18.1 us per call instead of 10.3, the
+        # ones after it 10.3 again); one more untimed replay absorbs it.
+        graph.replay()
         torch.cuda.synchronize()
         start.record(stream)
         graph.replay()
         end.record(stream)
     torch.cuda.synchronize()
+    if info is not None:
+        info["warmup_calls"] = len(steps_fns) + (n_warm + 1) * reps
     us = start.elapsed_time(end) * 1000.0 / reps
     del graph
     return us
+
+
+def sample_steps(steps_fns, n_samples: int = 100, warmup_replays: int = 25, min_calls: int = 20):
+    """Per-call time distribution: capture max(min_calls, sets) calls cycling
+    through the input sets in a HIP graph (every set read at least once per
+    replay, so each replay reads HBM; >= 20 calls so that the gap between
+    two replays is spread over enough calls), replay it `warmup_replays`
+    times, then `n_samples` times with an event recorded between replays on
+    the capture stream. Each sample is one replay's elapsed time over its
+    calls. Returns {median_us, p10_us, p90_us, samples, calls_per_sample}."""
+    import torch
+    calls = max(min_calls, len(steps_fns))
+    stream = torch.cuda.Stream()
+    # One eager call per set first: an op's per-stream workspace is allocated
+    # (and zeroed) on its first call, which must not land inside the graph.
+    with torch.cuda.stream(stream):
+        for fn in steps_fns:
+            fn()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(calls):
+            steps_fns[i % len(steps_fns)]()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(n_samples + 1)]
+    with torch.cuda.stream(stream):
+        for _ in range(warmup_replays):
+            graph.replay()
+        events[0].record(stream)
+        for i in range(n_samples):
+            graph.replay()
+            events[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_call = sorted(events[i].elapsed_time(events[i + 1]) * 1000.0 / calls
+                      for i in range(n_samples))
+    del graph
+
+    def q(f):
+        return round(per_call[min(n_samples - 1, int(f * n_samples))], 3)
+    return {"median_us": q(0.5), "p10_us": q(0.1), "p90_us": q(0.9), "samples": n_samples,
+            "calls_per_sample": calls}
 
 
 def n_sets_for(bytes_per_set: int) -> int:
@@ -200,7 +282,9 @@ def bench_attention(llmik, fmt: str, B: int, S: int, steps: int, warmup: int, gs
     else:
         fns = [lambda s=s: llmik.decode_attention_int4(s[0], s[1], s[2], s[3], s[4], gs, scale)
                for s in sets]
-    us = time_steps(fns, warmup, steps, all_sets=not exact_steps)
+    info = {}
+    us = time_steps(fns, warmup, steps, all_sets=not exact_steps, info=info)
+    dist = sample_steps(fns)
     del sets, fns
     torch.cuda.empty_cache()
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -208,7 +292,8 @@ def bench_attention(llmik, fmt: str, B: int, S: int, steps: int, warmup: int, gs
             "us": round(us, 3), "bytes": nbytes, "GBps": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "max_abs_err": err,
             "max_err_minus_out_half_ulp": excess, "sets": n_sets,
-            "rotated_MB": round(n_sets * nbytes / 1e6, 1)}
+            "rotated_MB": round(n_sets * nbytes / 1e6, 1), "dist": dist,
+            "warmup_calls": info["warmup_calls"]}
 
 
 def unpack_int4(p):
@@ -241,6 +326,7 @@ def bench_w4a16(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int 
     del ref, got
     fns = [lambda s=s: llmik.w4a16_gemm(s[0], s[1], s[2], gs) for s in sets]
     us = time_steps(fns, warmup, steps)
+    dist = sample_steps(fns)
     del sets, fns
     torch.cuda.empty_cache()
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -250,7 +336,7 @@ def bench_w4a16(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int 
             "GBps": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "TFLOPs": round(tf, 2), "frac_mfma_fp16_peak": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
             "max_abs_err_f32out": err, "sets": n_sets,
-            "rotated_MB": round(n_sets * nbytes / 1e6, 1)}
+            "rotated_MB": round(n_sets * nbytes / 1e6, 1), "dist": dist}
 
 
 def bench_prefill(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int = 128,
@@ -727,7 +813,10 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    # 16000 untimed calls (160 replays of the 100-call graph, ~0.4 s at A16):
+    # the sustained-load warm-up time_steps asks for ("warmup_calls" adds the
+    # eager call per input set and the settling replay).
+    ap.add_argument("--warmup", type=int, default=16000)
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
@@ -826,6 +915,7 @@ def main() -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_calls": head["warmup_calls"],
         "ms_per_step": round(head["us"] / 1000.0, 6),
         "higher_is_better": False,
         "scaling": "weak",
@@ -836,6 +926,8 @@ def main() -> None:
                    "batch": 8, "n_heads": 32, "n_kv_heads": 8, "head_dim": 128,
                    "seqlen_kv": 4096, "kv_layout": "[B, Hkv, S, D] fp16 contiguous",
                    "input_sets_rotated": head["sets"]},
+        # per-call distribution over 100 graph replays of >= 20 calls each
+        "dist": head["dist"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": head["bytes"]},

@@ -131,6 +131,35 @@ def test_int4_pipeline_matches_oracle(llmik, cuda, B, L, gs):
     assert _max_abs(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["int8", "int4g128", "int4g16"])
+@pytest.mark.parametrize("B,H,Hkv,L", [(2, 8, 8, 1500),     # MHA: one head per workgroup
+                                        (2, 16, 8, 1500),    # GQA 2: two heads per workgroup
+                                        (1, 24, 8, 2000)])   # GQA 3: one head, three head chunks
+def test_quantised_head_ratios_with_splits(llmik, cuda, fmt, B, H, Hkv, L):
+    """INT8 and INT4 at one, two and three query heads per KV head, with the
+    sequence split over several workgroups per head chunk (the split
+    hand-off's output ownership at one and two heads per workgroup). Group
+    16 runs the VALU kernel; 1500 tokens end inside a 128-token group."""
+    q, k, v = _inputs(B, H, Hkv, L, seed=H * 100 + L, outliers=True)
+    scale = 1 / math.sqrt(128)
+    if fmt == "int8":
+        kq_, ks = llmik.quantize_per_token(_dev(k, cuda))
+        vq_, vs = llmik.quantize_per_token(_dev(v, cuda))
+        out = llmik.decode_attention_int8(_dev(q, cuda), kq_, ks, vq_, vs, scale)
+        k_dq = kq.dequantize_per_token(kq_.cpu().numpy(), ks.cpu().numpy())
+        v_dq = kq.dequantize_per_token(vq_.cpu().numpy(), vs.cpu().numpy())
+    else:
+        gs = int(fmt[5:])
+        kq_, ks = llmik.quantize_k_per_channel_groupwise_int4(_dev(k, cuda), gs)
+        vq_, vs = llmik.quantize_v_per_token_int4(_dev(v, cuda))
+        out = llmik.decode_attention_int4(_dev(q, cuda), kq_, ks, vq_, vs, gs, scale)
+        k_dq = kq.dequantize_per_channel_groupwise(kq.unpack_kv_int4(kq_.cpu().numpy()),
+                                                   ks.cpu().numpy(), gs)
+        v_dq = kq.dequantize_per_token(kq.unpack_kv_int4(vq_.cpu().numpy()), vs.cpu().numpy())
+    assert out.shape == (B, H, 128)
+    assert _max_abs(out, oa.decode_attention(q, k_dq, v_dq, scale)) <= TOL
+
+
 def test_int4_large_batch_config_properties(llmik, cuda):
     """B=64, S=8192 (the second INT4 config): parity on a sample of batches
     (the oracle is run per batch row) and a batch-permutation property."""
