@@ -669,9 +669,9 @@ def bench_floors(steps: int, warmup: int) -> list:
     in all). Each read size runs at every grid in FLOOR_GRIDS (workgroups of
     8 waves) and every depth in FLOOR_LOADS (16-byte loads per lane in
     flight); the empty kernel at 256 and 1024 workgroups. Rows are printed
-    in the order their dispatches run: for each, max(warmup, windows) eager
-    calls, then two graph replays of max(steps, windows) calls. A last row
-    per size names the fastest read."""
+    in the order their dispatches run; "calls" counts a row's dispatches
+    (time_steps' untimed calls, then the timed replay of "reps" calls, which
+    are the row's last). A last row per size names the fastest read."""
     import torch
     from llmik_cuda._lib import check, lib
     dev = torch.device("cuda:0")
@@ -682,9 +682,10 @@ def bench_floors(steps: int, warmup: int) -> list:
 
     for nwg in (256, 1024):
         fn = (lambda n=nwg: check(lib.llmik_diag_empty(n, stream_ptr())))
-        us = time_steps([fn], warmup, steps)
+        info = {}
+        us = time_steps([fn], warmup, steps, info=info)
         rows.append({"name": f"empty kernel, {nwg} x 512 threads", "n_workgroups": nwg,
-                     "calls": max(warmup, 1) + 2 * steps, "us": round(us, 3)})
+                     "calls": info["warmup_calls"] + steps, "reps": steps, "us": round(us, 3)})
         log(rows[-1])
     for name, nbytes in FLOOR_SIZES:
         nbytes = (nbytes + 255) // 256 * 256
@@ -698,10 +699,12 @@ def bench_floors(steps: int, warmup: int) -> list:
                         check(lib.llmik_diag_read(ctypes.c_void_p(buf.data_ptr() + i * nbytes), nbytes,
                                                   ctypes.c_void_p(sk.data_ptr()), n, L, stream_ptr())))
                        for i in range(n_sets)]
-                us = time_steps(fns, warmup, steps)
+                info = {}
+                us = time_steps(fns, warmup, steps, info=info)
+                reps = max(steps, n_sets)
                 size_rows.append({"name": f"read {name}", "bytes": nbytes, "n_workgroups": nwg,
                                   "loads_per_lane": L, "windows": n_sets,
-                                  "calls": max(warmup, n_sets) + 2 * max(steps, n_sets),
+                                  "calls": info["warmup_calls"] + reps, "reps": reps,
                                   "us": round(us, 3), "TBps": round(nbytes / us / 1e6, 3)})
                 log(size_rows[-1])
         best = min(size_rows, key=lambda r: r["us"])
