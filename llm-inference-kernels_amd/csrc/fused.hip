@@ -194,18 +194,26 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __rest
                                                           uint16_t* __restrict__ out, int hidden,
                                                           float eps) {
     const long row = blockIdx.x;
-    u32x4 hv[NV], wv[NV];
+    // Every load is issued before any is used, so the kernel waits on memory
+    // once (with the h stores between the loads of two rounds, the compiler
+    // waited twice).
+    u32x4 xa[NV], ra[NV], hv[NV], wv[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int i = (threadIdx.x + 256 * k) * 8;
         const bool ok = i < hidden;
         const u32x4 z{0u, 0u, 0u, 0u};
-        const u32x4 xa = ok ? load16(x + row * hidden + i) : z;
-        const u32x4 ra = ok ? load16(r + row * hidden + i) : z;
+        xa[k] = ok ? load16(x + row * hidden + i) : z;
+        ra[k] = ok ? load16(r + row * hidden + i) : z;
         wv[k] = ok ? load16(w + i) : z;
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = (threadIdx.x + 256 * k) * 8;
+        const bool ok = i < hidden;
         float a[8], c[8];
-        f16x8_to_f32(xa, a);
-        f16x8_to_f32(ra, c);
+        f16x8_to_f32(xa[k], a);
+        f16x8_to_f32(ra[k], c);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             hv[k][e] = (uint32_t)f2h_bits(a[2 * e] + c[2 * e]) |
