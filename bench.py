@@ -373,6 +373,34 @@ def bench_prefill(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: in
     return kern
 
 
+def bench_fp16_library_gemm(llmik, M: int, K: int, N: int, steps: int, warmup: int, gs: int = 128,
+                            seed: int = 0) -> dict:
+    """A reference point for the MFMA-bound W4A16 rows: the same product with
+    the weights already dequantised to fp16 (w4a16_dequantize, outside the
+    timed region) and multiplied by torch.matmul (hipBLASLt) over rotating
+    sets of fp16 weights (4x the int4 weight bytes per call). It is the
+    vendor library's time for the GEMM alone, with no dequantisation cost."""
+    import torch
+    dev = torch.device("cuda:0")
+    nbytes = 2 * K * N + 2 * M * K + 2 * M * N
+    n_sets = n_sets_for(nbytes)
+    gen = torch.Generator(device=dev).manual_seed(seed + 2)
+    sets = []
+    for _ in range(n_sets):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), generator=gen, device=dev,
+                          dtype=torch.int32)
+        sc = (torch.rand((K // gs, N), generator=gen, device=dev) * 0.004 + 0.001).half()
+        sets.append((torch.randn((M, K), generator=gen, device=dev, dtype=torch.float16),
+                     llmik.w4a16_dequantize(w, sc, gs)))
+        del w, sc
+    fns = [lambda s=s: torch.matmul(s[0], s[1]) for s in sets]
+    us = time_steps(fns, warmup, steps)
+    del sets, fns
+    torch.cuda.empty_cache()
+    return {"fp16_library_gemm_us": round(us, 3),
+            "fp16_library_gemm_TFLOPs": round(2.0 * M * K * N / (us * 1e-6) / 1e12, 2)}
+
+
 def bench_decode_layer(llmik, n_layers: int, B: int, ctx: int, steps: int, warmup: int,
                        fused: bool = True) -> dict:
     """A decode step through `n_layers` Llama-3-8B layers (llmik_cuda.decode_layer:
@@ -880,6 +908,8 @@ def main() -> None:
             for M in (1, 16, 128):
                 for K, N in ((4096, 4096), (4096, 14336), (14336, 4096)):
                     details.append(bench_w4a16(llmik, M, K, N, 100 if M < 128 else 30, 10, seed=6))
+                    if M == 128:
+                        details[-1].update(bench_fp16_library_gemm(llmik, M, K, N, 30, 10, seed=6))
                     log(details[-1])
         if want("prefill"):
             for M in (256, 2048):
