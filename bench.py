@@ -31,8 +31,9 @@ Method
     own events.
   * Before timing, every config is checked against a float64 torch
     computation on the GPU (max-abs 2e-3); a failing config aborts the run.
-  * roofline.achieved = algorithmic bytes per launch / per-launch time, with
-    the byte counts stated in DESIGN.md; peak = 8 TB/s (MI355X HBM3E).
+  * roofline.achieved = algorithmic bytes per launch / per-launch time, the
+    bytes counting each tensor once (attn_bytes, w4a16_bytes: K and V once per
+    KV head, plus q, out and scales); peak = 8 TB/s (MI355X HBM3E).
   * cpu_baseline: the reference's eager fp32 attention restated with torch
     CPU ops (oracle/torch_ref.py: repeat_interleave GQA, fp32 matmul,
     softmax, matmul, .to(fp16)) on the host cores given by
