@@ -28,7 +28,9 @@ Method
   * Each attention and W4A16 row also carries "dist": the median, p10 and
     p90 per-call time over 100 replays (after 25 warm-up replays) of a graph
     of max(20, sets) calls over the input sets, each replay bracketed by its
-    own events.
+    own events. Full rows go to stderr as they are measured; the JSON line
+    carries a compact {row: {us, frac, ...}} per config ("details") so that
+    it stays a few KB long.
   * Before timing, every config is checked against a float64 torch
     computation on the GPU (max-abs 2e-3); a failing config aborts the run.
   * roofline.achieved = algorithmic bytes per launch / per-launch time, the
@@ -683,11 +685,21 @@ def cpu_details(budget_s: float = 3.0):
 FLOOR_SIZES = (
     ("w4a16 (4096, 4096) M=1", w4a16_bytes(1, 4096, 4096)),
     ("w4a16 (4096, 14336) M=1", w4a16_bytes(1, 4096, 14336)),
+    ("attention INT4 g128 B=8 S=4096", attn_bytes("int4", 8, 32, 8, 4096)),
+    ("attention INT8 B=8 S=4096", attn_bytes("int8", 8, 32, 8, 4096)),
     ("attention A16 K and V", 2 * 8 * 8 * 4096 * 128 * 2),
     ("1 GiB", 1 << 30),
 )
 FLOOR_GRIDS = (256, 1024, 2048)
 FLOOR_LOADS = (4, 8, 16)
+# Read + write streams of the KV writers at B=8, S=4096 (one fp16 tensor in,
+# codes out; the scales' 0.5 MB are left out): (name, bytes read, bytes
+# written per 16 read).
+FLOOR_RW = (
+    ("INT8 per-token writer stream", 8 * 8 * 4096 * 128 * 2, 8),
+    ("INT4 writer stream", 8 * 8 * 4096 * 128 * 2, 4),
+)
+FLOOR_RW_LOADS = (4, 8)
 
 
 def bench_floors(steps: int, warmup: int) -> list:
@@ -742,6 +754,34 @@ def bench_floors(steps: int, warmup: int) -> list:
                      "TBps": best["TBps"], "n_workgroups": best["n_workgroups"],
                      "loads_per_lane": best["loads_per_lane"]})
         del buf
+        torch.cuda.synchronize()
+    for name, nbytes, wb in FLOOR_RW:
+        out_bytes = nbytes // 16 * wb
+        n_sets = n_sets_for(nbytes + out_bytes)
+        src = torch.randint(0, 256, (n_sets * nbytes,), dtype=torch.uint8, device=dev)
+        dst = torch.empty((n_sets * out_bytes,), dtype=torch.uint8, device=dev)
+        size_rows = []
+        for nwg in FLOOR_GRIDS:
+            for L in FLOOR_RW_LOADS:
+                fns = [(lambda i=i, n=nwg, L=L:
+                        check(lib.llmik_diag_read_write(ctypes.c_void_p(src.data_ptr() + i * nbytes), nbytes,
+                                                        ctypes.c_void_p(dst.data_ptr() + i * out_bytes), wb,
+                                                        n, L, stream_ptr())))
+                       for i in range(n_sets)]
+                info = {}
+                us = time_steps(fns, warmup, steps, info=info)
+                reps = max(steps, n_sets)
+                size_rows.append({"name": f"read+write {name}", "bytes_read": nbytes,
+                                  "bytes_written": out_bytes, "n_workgroups": nwg, "loads_per_lane": L,
+                                  "windows": n_sets, "calls": info["warmup_calls"] + reps, "reps": reps,
+                                  "us": round(us, 3), "TBps": round((nbytes + out_bytes) / us / 1e6, 3)})
+                log(size_rows[-1])
+        best = min(size_rows, key=lambda r: r["us"])
+        rows.extend(size_rows)
+        rows.append({"name": f"fastest read+write {name}", "bytes_read": nbytes, "bytes_written": out_bytes,
+                     "us": best["us"], "TBps": best["TBps"], "n_workgroups": best["n_workgroups"],
+                     "loads_per_lane": best["loads_per_lane"]})
+        del src, dst
         torch.cuda.synchronize()
     return rows
 
@@ -837,6 +877,27 @@ def read_traffic():
     if len(vals) != 2:
         return None
     return vals["fetch_bytes_per_launch"] + vals["write_bytes_per_launch"]
+
+
+# ------------------------------------------------------- compact JSON rows
+
+_SHAPE_KEYS = ("fmt", "M", "K", "N", "B", "S", "layers", "ctx", "new_tokens", "residual_tokens")
+_VALUE_KEYS = (("us", "us"), ("frac_hbm_peak", "frac"), ("frac_mfma_fp16_peak", "mfma_frac"),
+               ("fp16_library_gemm_us", "lib_us"), ("dequant_matmul_us", "deq_lib_us"),
+               ("eager_us_per_layer", "eager_us"), ("graph_us_per_layer", "graph_us"),
+               ("max_abs_err", "err"), ("max_abs_err_f32out", "err"), ("cpu_us", "cpu_us"))
+
+
+def compact(rows) -> dict:
+    """{row key: {short value keys}} for the one-line JSON, so that every
+    config's time and roofline fraction fits in a few KB (the full rows, with
+    their distributions and byte counts, go to stderr as they are measured).
+    The key is the row name followed by its shape, e.g. "attn_int8 B8 S4096"."""
+    out = {}
+    for r in rows or []:
+        key = " ".join([r["name"]] + [f"{k}{r[k]}" for k in _SHAPE_KEYS if k in r])
+        out[key] = {short: r[k] for k, short in _VALUE_KEYS if k in r and r[k] is not None}
+    return out
 
 
 # ---------------------------------------------------------------------- main
@@ -964,13 +1025,17 @@ def main() -> None:
         "dist": head["dist"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "traffic_source": ("profiles/" + TRAFFIC_FILE.name + ": rocprofv3 --pmc FETCH_SIZE "
+                                        "+ WRITE_SIZE per headline launch, scaled by a copy of known "
+                                        "size; committed, not measured in this run"),
                      "algorithmic_bytes_per_launch": head["bytes"]},
         "cpu_baseline": cpu,
-        "cpu_details": cpu_more,
-        "details": details,
+        # every other config: {row: {us, frac of 8 TB/s, ...}}; full rows on stderr
+        "details": compact(details),
+        "cpu_details": compact(cpu_more),
         "gpu_wall_s": round(gpu_wall, 1),
     }
-    print(json.dumps(line))
+    print(json.dumps(line, separators=(",", ":")))
 
 
 if __name__ == "__main__":

@@ -441,6 +441,15 @@ LLMIK_API llmik_status llmik_silu_mul_halves(const void* gate_up, void* out, lon
 LLMIK_API llmik_status llmik_diag_empty(int n_workgroups, void* stream);
 LLMIK_API llmik_status llmik_diag_read(const void* src, size_t bytes, void* sink, int n_workgroups,
                                        int loads_per_lane, void* stream);
+/*
+ * llmik_diag_read_write: the read of llmik_diag_read (loads_per_lane 4 or 8)
+ * with a write stream of write_bytes_per_16 (4, 8 or 16) bytes per 16 bytes
+ * read: 16-byte chunk j of src gives its first write_bytes_per_16 bytes to
+ * dst at j * write_bytes_per_16 (src, dst 16-byte aligned; dst holds
+ * bytes / 16 * write_bytes_per_16 bytes). The KV writers' stream shape.
+ */
+LLMIK_API llmik_status llmik_diag_read_write(const void* src, size_t bytes, void* dst, int write_bytes_per_16,
+                                             int n_workgroups, int loads_per_lane, void* stream);
 
 #ifdef __cplusplus
 }

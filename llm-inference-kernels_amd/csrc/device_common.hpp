@@ -224,4 +224,35 @@ __device__ __forceinline__ float quant_round(float x, float s, float r) {
     return k;
 }
 
+// ---- torch's non-finite semantics for the symmetric quantisers ------------
+// |x| as bits. With the sign cleared, the unsigned order of the bit patterns
+// is the float order and every NaN sits above +inf, so an unsigned max over
+// them is torch's `x.abs().amax()`, which propagates NaN (fmaxf drops it).
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+
+// Unsigned max over the 16 lanes of a DPP row; every lane gets the result.
+__device__ __forceinline__ uint32_t row16_umax(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppQuadXor1, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppQuadXor2, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppRowHalfMirror, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppRowMirror, 0xF, 0xF, true));
+    return v;
+}
+
+// (absmax / qmax).clamp(min=1e-8) in fp32: a NaN absmax stays NaN (torch's
+// clamp keeps NaN), +inf stays +inf.
+__device__ __forceinline__ float sym_scale(uint32_t absmax_bits, float qmax) {
+    const float s = __uint_as_float(absmax_bits) / qmax;
+    return s < 1.0e-8f ? 1.0e-8f : s;
+}
+
+// clamp(round(x / s), -qmax, qmax) as an integer code (r = 1 / s). A NaN
+// quotient (a NaN scale, or inf / inf) gives code 0, which is what torch's
+// float -> int8 conversion of NaN stores on x86; finite / inf is 0 already.
+__device__ __forceinline__ int sym_code(float x, float s, float r, float qmax) {
+    const float v = quant_round(x, s, r);
+    if (v != v) return 0;
+    return (int)fminf(fmaxf(v, -qmax), qmax);
+}
+
 }  // namespace llmik

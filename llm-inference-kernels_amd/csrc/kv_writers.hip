@@ -4,6 +4,10 @@
 //   q     = clamp(round_half_even(x / scale), -qmax, qmax)
 //   scale stored as fp16 (round to nearest even)
 // (kv_cache_ref.py:46-62 per token, :73-112 per channel groupwise.)
+// Non-finite inputs follow torch: amax propagates NaN (kv_cache_ref.py:59-61)
+// and clamp keeps it, so a row (or group channel) holding a NaN stores scale
+// NaN and codes 0; one holding +-inf stores scale +inf, and every quotient is
+// then 0 (finite / inf) or NaN (inf / inf), whose int8 conversion is 0.
 // The reference CUDA writers multiply by an approximate reciprocal under
 // fast-math (kernels/kv_cache/kv_compress.cu:50-58,128-129,200-201) and are
 // only within +-1 code of the oracle; these kernels divide exactly.
@@ -70,20 +74,16 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
         const long flat = blk + 16 * i + rr;
         float xf[8];
         f16x8_to_f32(raw[i], xf);
-        float amax = 0.0f;
+        uint32_t amax = 0u;   // NaN-propagating absmax, as bits
 #pragma unroll
-        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xf[e]));
-        amax = row16_max(amax);
+        for (int e = 0; e < 8; ++e) amax = max(amax, abs_bits(xf[e]));
+        amax = row16_umax(amax);
 
-        const float sc = fmaxf(amax / (float)QMAX, 1.0e-8f);
+        const float sc = sym_scale(amax, (float)QMAX);
         const float rcp = 1.0f / sc;
         int code[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = quant_round(xf[e], sc, rcp);
-            v = fminf(fmaxf(v, -(float)QMAX), (float)QMAX);
-            code[e] = (int)v;
-        }
+        for (int e = 0; e < 8; ++e) code[e] = sym_code(xf[e], sc, rcp, (float)QMAX);
         if (flat < rows) {
             const long row = MAPPED ? map.dst((uint32_t)flat) : flat;
             if constexpr (PACK4) {
@@ -130,27 +130,27 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
         const int t = min(t_start + row + 16 * i, t_end - 1);   // in bounds; duplicates do not move the max
         raw[i] = stream16(x + (base + t) * 128 + 8 * c);
     }
-    float amax[8];
+    uint32_t amax[8];   // NaN-propagating absmax per channel, as bits
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax[e] = 0.0f;
+    for (int e = 0; e < 8; ++e) amax[e] = 0u;
 #pragma unroll
     for (int i = 0; i < TPR; ++i) {
         float xf[8];
         f16x8_to_f32(raw[i], xf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) amax[e] = fmaxf(amax[e], fabsf(xf[e]));
+        for (int e = 0; e < 8; ++e) amax[e] = max(amax[e], abs_bits(xf[e]));
     }
 
-    __shared__ float s_max[16][128];
+    __shared__ uint32_t s_max[16][128];
     __shared__ float s_scale[128];
 #pragma unroll
     for (int e = 0; e < 8; ++e) s_max[row][8 * c + e] = amax[e];
     __syncthreads();
     if (threadIdx.x < 128) {
-        float m = 0.0f;
+        uint32_t m = 0u;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) m = fmaxf(m, s_max[r][threadIdx.x]);
-        const float sc = fmaxf(m / 7.0f, 1.0e-8f);
+        for (int r = 0; r < 16; ++r) m = max(m, s_max[r][threadIdx.x]);
+        const float sc = sym_scale(m, 7.0f);
         s_scale[threadIdx.x] = sc;
         scale[sslot * 128 + threadIdx.x] = f2h_bits(sc);
     }
@@ -169,11 +169,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
         f16x8_to_f32(raw[i], xf);
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = quant_round(xf[e], sv[e], rcp[e]);
-            v = fminf(fmaxf(v, -7.0f), 7.0f);
-            w |= (uint32_t)((int)v & 0xF) << (4 * e);
-        }
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7.0f) & 0xF) << (4 * e);
         if (t < t_end)
             __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(q + (qbase + t) * 64 + 4 * c));
     }
@@ -195,26 +191,26 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_larg
     const long qbase = bh * map.dst_len + map.dst_off;      // cache row of token 0
     const long sslot = bh * dst_groups + map.dst_off / group_size + g;
 
-    float amax[8];
+    uint32_t amax[8];   // NaN-propagating absmax per channel, as bits
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax[e] = 0.0f;
+    for (int e = 0; e < 8; ++e) amax[e] = 0u;
     for (int t = t_start + row; t < t_end; t += 16) {
         float xf[8];
         f16x8_to_f32(load16(x + (base + t) * 128 + 8 * c), xf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) amax[e] = fmaxf(amax[e], fabsf(xf[e]));
+        for (int e = 0; e < 8; ++e) amax[e] = max(amax[e], abs_bits(xf[e]));
     }
 
-    __shared__ float s_max[16][128];
+    __shared__ uint32_t s_max[16][128];
     __shared__ float s_scale[128];
 #pragma unroll
     for (int e = 0; e < 8; ++e) s_max[row][8 * c + e] = amax[e];
     __syncthreads();
     if (threadIdx.x < 128) {
-        float m = 0.0f;
+        uint32_t m = 0u;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) m = fmaxf(m, s_max[r][threadIdx.x]);
-        const float sc = fmaxf(m / 7.0f, 1.0e-8f);
+        for (int r = 0; r < 16; ++r) m = max(m, s_max[r][threadIdx.x]);
+        const float sc = sym_scale(m, 7.0f);
         s_scale[threadIdx.x] = sc;
         scale[sslot * 128 + threadIdx.x] = f2h_bits(sc);
     }
@@ -231,11 +227,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_larg
         f16x8_to_f32(load16(x + (base + t) * 128 + 8 * c), xf);
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = quant_round(xf[e], sv[e], rcp[e]);
-            v = fminf(fmaxf(v, -7.0f), 7.0f);
-            w |= (uint32_t)((int)v & 0xF) << (4 * e);
-        }
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7.0f) & 0xF) << (4 * e);
         *reinterpret_cast<uint32_t*>(q + (qbase + t) * 64 + 4 * c) = w;
     }
 }
@@ -321,27 +313,27 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
     }
     if (row == (r & 15)) *reinterpret_cast<u32x4*>(kopen + (long)r * 128) = knew;
 
-    float amax[8];
+    uint32_t amax[8];   // NaN-propagating absmax per channel, as bits
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax[e] = 0.0f;
+    for (int e = 0; e < 8; ++e) amax[e] = 0u;
 #pragma unroll
     for (int i = 0; i < TPR; ++i) {
         float xf[8];
         f16x8_to_f32(raw[i], xf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) amax[e] = fmaxf(amax[e], fabsf(xf[e]));
+        for (int e = 0; e < 8; ++e) amax[e] = max(amax[e], abs_bits(xf[e]));
     }
-    __shared__ float s_max[16][128];
+    __shared__ uint32_t s_max[16][128];
     __shared__ float s_scale[128];
 #pragma unroll
     for (int e = 0; e < 8; ++e) s_max[row][8 * c + e] = amax[e];
     __syncthreads();
     const int start = pos - r;
     if (threadIdx.x < 128) {
-        float m = 0.0f;
+        uint32_t m = 0u;
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) m = fmaxf(m, s_max[rr][threadIdx.x]);
-        const float sc = fmaxf(m / 7.0f, 1.0e-8f);
+        for (int rr = 0; rr < 16; ++rr) m = max(m, s_max[rr][threadIdx.x]);
+        const float sc = sym_scale(m, 7.0f);
         s_scale[threadIdx.x] = sc;
         k_scale[(bh * n_groups + start / group_size) * 128 + threadIdx.x] = f2h_bits(sc);
     }
@@ -359,11 +351,7 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
         f16x8_to_f32(raw[i], xf);
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = quant_round(xf[e], sv[e], rcp[e]);
-            v = fminf(fmaxf(v, -7.0f), 7.0f);
-            w |= (uint32_t)((int)v & 0xF) << (4 * e);
-        }
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7.0f) & 0xF) << (4 * e);
         if (t <= r) *reinterpret_cast<uint32_t*>(k_q + (bh * max_len + start + t) * 64 + 4 * c) = w;
     }
 
@@ -371,19 +359,15 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
     if (row == 0) {
         float xf[8];
         f16x8_to_f32(load16(v_in + bh * v_stride + 8 * c), xf);
-        float amax1 = 0.0f;
+        uint32_t amax1 = 0u;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) amax1 = fmaxf(amax1, fabsf(xf[e]));
-        amax1 = row16_max(amax1);
-        const float sc = fmaxf(amax1 / 7.0f, 1.0e-8f);
+        for (int e = 0; e < 8; ++e) amax1 = max(amax1, abs_bits(xf[e]));
+        amax1 = row16_umax(amax1);
+        const float sc = sym_scale(amax1, 7.0f);
         const float rc = 1.0f / sc;
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = quant_round(xf[e], sc, rc);
-            v = fminf(fmaxf(v, -7.0f), 7.0f);
-            w |= (uint32_t)((int)v & 0xF) << (4 * e);
-        }
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sc, rc, 7.0f) & 0xF) << (4 * e);
         *reinterpret_cast<uint32_t*>(v_q + (bh * max_len + pos) * 64 + 4 * c) = w;
         if (c == 0) v_scale[bh * max_len + pos] = f2h_bits(sc);
     }

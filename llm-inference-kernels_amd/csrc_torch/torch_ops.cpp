@@ -38,9 +38,24 @@ inline void check(llmik_status st) {
 }
 
 // ---- per-(device, stream) workspace ------------------------------------------
+// The kernels need the workspace's completion counters to be zero when they
+// start and leave them zero when they end. A buffer created eagerly is zeroed
+// before any kernel can use it, and is cached for the stream. A buffer created
+// while the stream is capturing a graph is zeroed only inside that graph (the
+// fill is recorded, not run), so it is right for that graph's replays alone:
+// it is kept alive for them but never cached, and a later call (eager, or in
+// another capture) on the stream gets a buffer of its own.
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Tensor> g_ws;
 std::vector<Tensor> g_ws_retired;
+std::vector<Tensor> g_ws_captured;
+
+bool stream_is_capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(s, &cs);
+    TORCH_CHECK(e == hipSuccess, "llmik: hipStreamIsCapturing failed: ", hipGetErrorString(e));
+    return cs != hipStreamCaptureStatusNone;
+}
 
 std::pair<void*, size_t> workspace(const Tensor& like, hipStream_t s, size_t nbytes) {
     if (nbytes == 0) return {nullptr, 0};
@@ -48,6 +63,11 @@ std::pair<void*, size_t> workspace(const Tensor& like, hipStream_t s, size_t nby
     std::lock_guard<std::mutex> lock(g_ws_mu);
     auto it = g_ws.find(key);
     if (it == g_ws.end() || (size_t)it->second.numel() < nbytes) {
+        if (stream_is_capturing(s)) {
+            Tensor ws = at::zeros({(int64_t)nbytes}, like.options().dtype(at::kByte));
+            g_ws_captured.push_back(ws);
+            return {ws.data_ptr(), nbytes};
+        }
         size_t size = nbytes;
         if (it != g_ws.end()) {
             size = std::max(nbytes, (size_t)(2 * it->second.numel()));

@@ -7,12 +7,15 @@ is an ImportError: there is no fallback path.
 from __future__ import annotations
 
 import ctypes
-import os
 from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime first)
 
-LIB_PATH = Path(os.environ.get("LLMIK_LIB", Path(__file__).resolve().parent / "libllmik_hip.so"))
+# Always the in-package library: _C links this same file (through an $ORIGIN
+# rpath), so the dynamic loader maps one copy and ctypes calls (plan
+# overrides, the last-error text, the no-alloc scratch) reach the state the
+# ops use.
+LIB_PATH = Path(__file__).resolve().parent / "libllmik_hip.so"
 
 if not LIB_PATH.exists():
     raise ImportError(
@@ -65,6 +68,7 @@ _SIGNATURES = {
     "llmik_add_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _p]),
     "llmik_diag_empty": (_i, [_i, _p]),
     "llmik_diag_read": (_i, [_p, _sz, _p, _i, _i, _p]),
+    "llmik_diag_read_write": (_i, [_p, _sz, _p, _i, _i, _i, _p]),
     "llmik_silu_mul_halves": (_i, [_p, _p, _l, _i, _p]),
 }
 

@@ -221,9 +221,13 @@ class DecodeLayer:
     def capture(self, x: torch.Tensor, pos: int, warmup: int = 2) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
         """Record `step(x, pos)` in a CUDA (HIP) graph. Returns the graph and
         its output tensor; `graph.replay()` reruns the step on whatever `x`
-        holds then. The warm-up steps on the capture stream set up the
-        module's per-stream workspace before capture."""
-        return _capture(self.step, x, pos, warmup)
+        holds then. Every capture of this layer runs on the layer's own
+        capture stream, whose split-K workspace the warm-up steps set up
+        before the first capture; all of the layer's graphs share that
+        workspace, so their replays must not overlap (replay them on one
+        stream, or order them)."""
+        self._capture_stream = _capture_stream(self, x.device)
+        return _capture(self.step, x, pos, warmup, self._capture_stream)
 
 
 class DecodeStack:
@@ -246,12 +250,26 @@ class DecodeStack:
         return h + r
 
     def capture(self, x: torch.Tensor, pos: int, warmup: int = 2) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
-        """As DecodeLayer.capture, for the whole stack."""
-        return _capture(self.step, x, pos, warmup)
+        """As DecodeLayer.capture, for the whole stack (one capture stream
+        per stack)."""
+        self._capture_stream = _capture_stream(self, x.device)
+        return _capture(self.step, x, pos, warmup, self._capture_stream)
 
 
-def _capture(step, x: torch.Tensor, pos: int, warmup: int) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
-    stream = torch.cuda.Stream(device=x.device)
+def _capture_stream(module, device: torch.device) -> torch.cuda.Stream:
+    """The module's capture stream, created on its first capture. The ops
+    cache their split-K workspace per stream, so graphs captured on one
+    stream share it. torch hands out streams from a pool of 32 per device,
+    so modules beyond that may share a stream handle; graphs whose capture
+    streams share a handle must likewise be replayed in one stream order."""
+    s = getattr(module, "_capture_stream", None)
+    if s is None or s.device != device:
+        s = torch.cuda.Stream(device=device)
+    return s
+
+
+def _capture(step, x: torch.Tensor, pos: int, warmup: int,
+             stream: torch.cuda.Stream) -> Tuple[torch.cuda.CUDAGraph, torch.Tensor]:
     stream.wait_stream(torch.cuda.current_stream(x.device))
     with torch.cuda.stream(stream):
         for _ in range(warmup):

@@ -91,9 +91,14 @@ def llmik_attention_forward(module: nn.Module, query: torch.Tensor, key: torch.T
     """transformers 5 attention function: query [B, H, q_len, D], key/value
     [B, Hkv, S, D] (or a KIVI layer's packed buffers) -> ([B, q_len, H, D], None)."""
     scale = float(scaling) if scaling is not None else query.shape[-1] ** -0.5
+    # The decode kernels compute plain softmax(scale q K^T) V over the whole
+    # live cache (the reference hooks Llama only): logit soft-capping,
+    # attention sinks (s_aux), sliding windows and additive position biases
+    # take the SDPA path.
+    plain = all(kwargs.get(name) is None for name in ("softcap", "s_aux", "sliding_window", "position_bias"))
     decode = (query.dim() == 4 and query.shape[2] == 1 and query.shape[-1] == 128
               and query.dtype == torch.float16 and query.is_cuda and attention_mask is None
-              and not dropout and not kwargs.get("output_attentions", False))
+              and not dropout and not kwargs.get("output_attentions", False) and plain)
     out = None
     if key.dtype == torch.int8:
         layer = _KIVI_LAYERS.get(key.data_ptr())

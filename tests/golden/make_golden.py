@@ -3,8 +3,9 @@ Python oracles (run once, in the build container, on the CPU).
 
 Only the quantisers are taken from the reference this way: their bit-level
 behaviour under torch's dtype rules (fp16-input scales rounded before the
-division, clamp(min=1e-8) in fp16, NaN codes of all-zero fp16 rows) is not
-fixed by any closed form. Attention is pinned by float64 brute force and
+division, clamp(min=1e-8) in fp16, NaN codes of all-zero fp16 rows, and
+rows holding NaN or +-inf, whose amax propagates NaN) is not fixed by any
+closed form. Attention is pinned by float64 brute force and
 closed forms instead and is not imported.
 
 Functions used (bundle-adjuster/llm-inference-kernels):
@@ -78,6 +79,44 @@ def kv_input(rng: np.random.Generator, shape) -> np.ndarray:
     return x
 
 
+def nonfinite_kv(rng: np.random.Generator):
+    """Per-token and group-wise inputs holding NaN, +-inf and fp16 overflow
+    (1e5 rounds to inf in fp16), at fixed places."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    pt = rng.standard_normal((1, 2, 8, 128)).astype(np.float32)
+    pt[..., list(OUTLIER_CHANNELS)] *= 10.0
+    pt[0, 0, 0, 5] = nan
+    pt[0, 0, 1, 7] = inf
+    pt[0, 0, 2, 9] = -inf
+    pt[0, 0, 3, :] = nan
+    pt[0, 0, 4, 3], pt[0, 0, 4, 4] = inf, nan
+    pt[0, 0, 5, 1], pt[0, 0, 5, 2] = inf, -inf
+    pt[0, 0, 7, :] = 0.0
+    pt[0, 1, 0, 127] = nan
+    pt[0, 1, 3, 64] = 1.0e5
+    pt[0, 1, 7, 0] = -inf
+    gw = rng.standard_normal((1, 2, 100, 128)).astype(np.float32)
+    gw[..., list(OUTLIER_CHANNELS)] *= 10.0
+    gw[0, 0, 5, 3] = nan           # group 0 (g32, g128), channel 3
+    gw[0, 0, 40, 10] = inf         # group 1 at g32
+    gw[0, 0, 99, 20] = -inf        # the short last group
+    gw[0, 0, 64:96, 30] = nan      # a whole g32 group of one channel
+    gw[0, 1, 64, 64] = 1.0e5       # inf once rounded to fp16
+    gw[0, 1, 10, 100], gw[0, 1, 11, 100] = inf, -inf
+    return pt, gw
+
+
+def nonfinite_w(rng: np.random.Generator) -> np.ndarray:
+    W = (rng.standard_normal((256, 96)) * 0.02).astype(np.float32)
+    W[3, 4] = np.nan
+    W[130, 7] = np.inf
+    W[200, 8] = -np.inf
+    W[0:64, 10] = np.nan           # a whole g64 group of one column
+    W[70, 11], W[71, 11] = np.inf, np.nan
+    W[150, 12] = 1.0e5             # inf once rounded to fp16
+    return W
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reference", default="/root/reference")
@@ -110,6 +149,27 @@ def main() -> None:
                 q, s = quantize_per_channel_groupwise(xt, bits, gs)
                 kv[f"{name}_b{bits}_g{gs}_q"] = q.numpy()
                 kv[f"{name}_b{bits}_g{gs}_s"] = s.numpy()
+
+    # Non-finite rows (own generator, so the arrays above do not move). The
+    # KV kernels take fp16 and follow the x.float() convention; both dtype
+    # conventions are stored.
+    nrng = np.random.default_rng(20261202)
+    pt_nf, gw_nf = nonfinite_kv(nrng)
+    kv["nf_pt_x32"], kv["nf_gw_x32"] = pt_nf, gw_nf
+    for pre, x32 in (("nf_pt", pt_nf), ("nf_gw", gw_nf)):
+        x16 = x32.astype(np.float16)
+        conv = {f"{pre}_x32": torch.from_numpy(x32), f"{pre}_x16": torch.from_numpy(x16),
+                f"{pre}_x16f": torch.from_numpy(x16).float()}
+        for name, xt in conv.items():
+            for bits in (8, 4):
+                if pre == "nf_pt":
+                    q, s = quantize_per_token(xt, bits)
+                    kv[f"{name}_b{bits}_q"], kv[f"{name}_b{bits}_s"] = q.numpy(), s.numpy()
+                else:
+                    for gs in (32, 128):
+                        q, s = quantize_per_channel_groupwise(xt, bits, gs)
+                        kv[f"{name}_b{bits}_g{gs}_q"] = q.numpy()
+                        kv[f"{name}_b{bits}_g{gs}_s"] = s.numpy()
     np.savez_compressed(HERE / "kv_quant_golden.npz", **kv)
 
     w = {}
@@ -134,6 +194,15 @@ def main() -> None:
     out = quantized_matmul_ref(torch.from_numpy(act), torch.from_numpy(w["W16_g128_q"]),
                                torch.from_numpy(w["W16_g128_s"]), 128)
     w["mm_out16"] = out.numpy()
+    Wn = nonfinite_w(np.random.default_rng(20261203))
+    w["Wn32"] = Wn
+    w["Wn16"] = Wn.astype(np.float16)
+    for name in ("Wn32", "Wn16"):
+        for gs in (64, 128):
+            q, s = quantize_weights_int4_groupwise(torch.from_numpy(w[name]), group_size=gs)
+            w[f"{name}_g{gs}_q"] = q.numpy()
+            w[f"{name}_g{gs}_s"] = s.numpy()
+            w[f"{name}_g{gs}_packed"] = pack_int4_along_k(q).numpy()
     np.savez_compressed(HERE / "w4a16_golden.npz", **w)
     print("wrote", HERE / "kv_quant_golden.npz", HERE / "w4a16_golden.npz")
 

@@ -196,12 +196,14 @@ def _sampled_rows_parity(out, q, k_rows, v_rows, rows, scale):
         assert _max_abs(out[b:b + 1], ref) <= TOL, f"batch row {b}"
 
 
-@pytest.mark.parametrize("B,L", [(8, 32768), (64, 4096)])
+@pytest.mark.parametrize("B,L", [(8, 1024), (8, 16384), (8, 32768), (1, 4096), (64, 4096)])
 def test_fp16_swept_baseline_configs(llmik, cuda, B, L):
-    """The fp16 sweep configs of the headline shape: B=8, S=32768 (the
-    longest chunks) and B=64, S=4096 (4-wave workgroups, 512 of them, no
-    split). Oracle parity on sampled batch rows and a batch permutation that
-    must permute the outputs bit for bit."""
+    """The fp16 sweep configs of the headline shape, each at its exact size:
+    B=8 at S=1024 (4-wave workgroups, two per CU), 16384 and 32768 (the
+    longest chunks), B=1 at S=4096 (16 eight-wave splits) and B=64 at
+    S=4096 (512 four-wave workgroups, no split). Oracle parity on sampled
+    batch rows and a batch permutation that must permute the outputs bit for
+    bit."""
     gen = torch.Generator(device=cuda).manual_seed(B + L)
     kd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
     vd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
@@ -210,7 +212,7 @@ def test_fp16_swept_baseline_configs(llmik, cuda, B, L):
     scale = 1 / math.sqrt(128)
     out = llmik.decode_attention(qd, kd, vd, scale)
     _sampled_rows_parity(out, q, lambda b: kd[b:b + 1].cpu().numpy(),
-                         lambda b: vd[b:b + 1].cpu().numpy(), (0, B // 2 - 1, B - 1), scale)
+                         lambda b: vd[b:b + 1].cpu().numpy(), sorted({0, max(0, B // 2 - 1), B - 1}), scale)
     perm = torch.randperm(B, generator=torch.Generator().manual_seed(1)).to(cuda)
     out_p = llmik.decode_attention(qd[perm].contiguous(), kd[perm].contiguous(),
                                    vd[perm].contiguous(), scale)

@@ -58,3 +58,33 @@ def test_empty_kernel_launches(cuda):
     for nwg in (1, 256, 1024):
         check(lib.llmik_diag_empty(nwg, _stream()))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("W", [4, 8, 16])
+@pytest.mark.parametrize("L", [4, 8])
+@pytest.mark.parametrize("nbytes,nwg", [(16, 1), (16000, 3), (1 << 20, 256), (4_194_304 + 4096, 2048)])
+def test_read_write_copies_the_leading_bytes(cuda, nbytes, nwg, L, W):
+    """llmik_diag_read_write writes the first W bytes of every 16-byte chunk
+    of src, in order, and nothing past bytes / 16 * W (a guard tail stays)."""
+    lib, check = _lib()
+    gen = torch.Generator(device=cuda).manual_seed(nbytes + W)
+    src = torch.randint(0, 256, (nbytes,), generator=gen, device=cuda, dtype=torch.uint8)
+    out_len = nbytes // 16 * W
+    dst = torch.full((out_len + 256,), 0xA5, dtype=torch.uint8, device=cuda)
+    check(lib.llmik_diag_read_write(ctypes.c_void_p(src.data_ptr()), nbytes, ctypes.c_void_p(dst.data_ptr()),
+                                    W, nwg, L, _stream()))
+    torch.cuda.synchronize()
+    want = src.cpu().numpy().reshape(-1, 16)[:, :W].reshape(-1)
+    got = dst.cpu().numpy()
+    assert np.array_equal(got[:out_len], want)
+    assert (got[out_len:] == 0xA5).all()
+
+
+def test_read_write_rejects_bad_arguments(cuda):
+    lib, _ = _lib()
+    buf = torch.zeros(1024, dtype=torch.int32, device=cuda)
+    p = ctypes.c_void_p(buf.data_ptr())
+    assert lib.llmik_diag_read_write(p, 100, p, 8, 1, 4, _stream()) != 0      # not a multiple of 16
+    assert lib.llmik_diag_read_write(p, 64, p, 5, 1, 4, _stream()) != 0       # write width
+    assert lib.llmik_diag_read_write(p, 64, p, 8, 1, 16, _stream()) != 0      # depth
+    assert lib.llmik_diag_read_write(p, 64, p, 8, 0, 4, _stream()) != 0

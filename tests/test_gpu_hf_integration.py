@@ -174,3 +174,27 @@ def test_fused_ops_patch(hf, cuda):
     after = _run(model, DynamicCache(), prompt, steps)
     assert torch.equal(after, ref)               # the originals are restored
     assert float((got - ref).abs().max()) <= LOGIT_TOL
+
+
+def test_softcap_sinks_and_windows_take_the_sdpa_path(hf, cuda, monkeypatch):
+    """A decode-shaped call carrying logit soft-capping, attention sinks or a
+    sliding window is not what the decode kernels compute: it must return
+    SDPA's result and never reach decode_attention."""
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    calls = _counting(monkeypatch, hf, "decode_attention")
+    g = torch.Generator(device=cuda).manual_seed(5)
+    q = torch.randn((2, 4, 1, 128), generator=g, device=cuda, dtype=torch.float16)
+    k = torch.randn((2, 2, 40, 128), generator=g, device=cuda, dtype=torch.float16)
+    v = torch.randn((2, 2, 40, 128), generator=g, device=cuda, dtype=torch.float16)
+    module = torch.nn.Module()
+    module.num_key_value_groups = 2
+    module.is_causal = True
+    plain, _ = hf.llmik_attention_forward(module, q, k, v, None, scaling=0.088)
+    assert calls["n"] == 1
+    for extra in ({"softcap": 5.0}, {"sliding_window": 16}):
+        got, _ = hf.llmik_attention_forward(module, q, k, v, None, scaling=0.088, **extra)
+        ref, _ = sdpa_attention_forward(module, q, k, v, None, scaling=0.088, **extra)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), extra
+    assert calls["n"] == 1
+    assert plain.shape == (2, 1, 4, 128)

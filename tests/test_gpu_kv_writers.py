@@ -125,3 +125,69 @@ def test_fp32_golden_rows_at_fp16_exact_values(llmik, cuda):
     q, s_ = llmik.quantize_per_token(_dev(x, cuda))
     rq, rs = kq.quantize_per_token(x.astype(np.float32), 8)
     assert _bits_equal(q, rq) and _bits_equal(s_, rs.astype(np.float16))
+
+
+def _bits_equal_nan(t: torch.Tensor, a: np.ndarray) -> bool:
+    """Bit-exact, except that a NaN matches any NaN (torch's own NaN payload
+    depends on its reduction path, so it is no pin)."""
+    got = t.cpu().numpy()
+    if got.shape != a.shape or got.dtype != a.dtype:
+        return False
+    ng, na = np.isnan(got), np.isnan(a)
+    return bool((ng == na).all()) and np.array_equal(got[~ng].view(np.uint8), a[~na].view(np.uint8))
+
+
+def _nonfinite16(key: str) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        return GOLD[key].astype(np.float16)
+
+
+def test_nonfinite_golden_rows(llmik, cuda):
+    """Rows holding NaN, +-inf and fp16 overflow, against the reference's
+    own quantisers on x.float() (tests/golden, kv_cache_ref.py:59-61): a row
+    (or group channel) with a NaN stores scale NaN and codes 0, one with an
+    inf stores +inf and codes 0, and every other row is unchanged."""
+    x16 = _nonfinite16("nf_pt_x32")
+    xd = _dev(x16, cuda)
+    q8, s8 = llmik.quantize_per_token(xd)
+    assert _bits_equal(q8, GOLD["nf_pt_x16f_b8_q"])
+    assert _bits_equal_nan(s8, GOLD["nf_pt_x16f_b8_s"].astype(np.float16))
+    q4, s4 = llmik.quantize_v_per_token_int4(xd)
+    assert _bits_equal(q4, kq.pack_kv_int4(GOLD["nf_pt_x16f_b4_q"]))
+    assert _bits_equal_nan(s4, GOLD["nf_pt_x16f_b4_s"].astype(np.float16))
+    assert torch.isnan(s8[0, 0, 3]) and torch.isinf(s8[0, 0, 1]) and not q8[0, 0, :6].any()
+    g16 = _dev(_nonfinite16("nf_gw_x32"), cuda)
+    for gs in (32, 128):
+        qk, sk = llmik.quantize_k_per_channel_groupwise_int4(g16, gs)
+        assert _bits_equal(qk, kq.pack_kv_int4(GOLD[f"nf_gw_x16f_b4_g{gs}_q"]))
+        assert _bits_equal_nan(sk, GOLD[f"nf_gw_x16f_b4_g{gs}_s"].astype(np.float16))
+    # The in-place forms (mapped token positions) and the one-launch KIVI
+    # append share the arithmetic; check them on the same rows.
+    qc = torch.full((1, 2, 12, 128), 0x5A, dtype=torch.int8, device=cuda)
+    sc = torch.full((1, 2, 12), 1234.0, dtype=torch.float16, device=cuda)
+    llmik.quantize_per_token_into(xd, qc, sc, 3)
+    assert torch.equal(qc[:, :, 3:11], q8)
+    assert torch.equal(torch.isnan(sc[:, :, 3:11]), torch.isnan(s8))
+    assert torch.equal(torch.nan_to_num(sc[:, :, 3:11]).view(torch.int16),
+                       torch.nan_to_num(s8).view(torch.int16))
+
+
+def test_nonfinite_kivi_append(llmik, cuda):
+    """Single-token appends through Int4KIVICache's one-launch path, where
+    the open K group and the V token hold NaN and inf: the cache holds what
+    the oracle quantisers give for the same fp16 tokens."""
+    from llmik_cuda.kv_cache import Int4KIVICache
+    g = 32
+    k_all = _nonfinite16("nf_gw_x32")[:, :, :40]          # NaN at token 5, inf at token 10/11
+    v_all = np.concatenate([_nonfinite16("nf_pt_x32")] * 5, axis=2)   # 40 tokens
+    cache = Int4KIVICache(1, 2, max_len=64, group_size=g, device=cuda)
+    for t in range(40):
+        cache.append(_dev(k_all[:, :, t:t + 1], cuda), _dev(v_all[:, :, t:t + 1], cuda))
+    k_q, k_s, v_q, v_s, L = cache.get_quantized_for_attention()
+    rq0, rs0 = kq.quantize_per_channel_groupwise(k_all[:, :, :32].astype(np.float32), 4, g)
+    rq1, rs1 = kq.quantize_per_channel_groupwise(k_all[:, :, 32:].astype(np.float32), 4, g)
+    rvq, rvs = kq.quantize_per_token(v_all.astype(np.float32), 4)
+    assert _bits_equal(k_q[:, :, :L], kq.pack_kv_int4(np.concatenate([rq0, rq1], axis=2)))
+    assert _bits_equal_nan(k_s[:, :, :2], np.concatenate([rs0, rs1], axis=2).astype(np.float16))
+    assert _bits_equal(v_q[:, :, :L], kq.pack_kv_int4(rvq))
+    assert _bits_equal_nan(v_s[:, :, :L], rvs.astype(np.float16))

@@ -52,6 +52,22 @@ def test_quantizer_matches_reference_golden(llmik, cuda, name, gs):
         assert np.array_equal(llmik.pack_int4_along_k(q).cpu().numpy(), GOLD[key])
 
 
+@pytest.mark.parametrize("name", ["Wn32", "Wn16"])
+@pytest.mark.parametrize("gs", [64, 128])
+def test_quantizer_nonfinite_matches_reference_golden(llmik, cuda, name, gs):
+    """Weights holding NaN, +-inf and fp16 overflow: torch's amax propagates
+    NaN (quant_matmul_ref.py:79-80), so a group column with a NaN stores
+    scale NaN, one with an inf +inf, and their codes are 0. NaN matches any
+    NaN (torch's payload depends on its reduction path)."""
+    W = _dev(GOLD[name], cuda)
+    q, s = llmik.quantize_weights_int4_groupwise(W, gs)
+    assert np.array_equal(q.cpu().numpy(), GOLD[f"{name}_g{gs}_q"])
+    got, ref = s.cpu().numpy(), GOLD[f"{name}_g{gs}_s"]
+    assert got.dtype == ref.dtype and np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(got)].view(np.uint8), ref[~np.isnan(ref)].view(np.uint8))
+    assert np.array_equal(llmik.pack_int4_along_k(q).cpu().numpy(), GOLD[f"{name}_g{gs}_packed"])
+
+
 @pytest.mark.parametrize("K,N,gs,dtype", [(4096, 512, 128, np.float32), (1024, 320, 64, np.float16),
                                           (1000, 96, 128, np.float32), (768, 130, 256, np.float16),
                                           (512, 64, 32, np.float32), (2048, 48, 32, np.float16)])

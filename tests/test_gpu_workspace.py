@@ -124,3 +124,52 @@ def test_graph_keeps_its_workspace_after_the_stream_grows(llmik, cuda):
     with torch.cuda.stream(stream):
         assert torch.equal(llmik.decode_attention(qb, kb, kb, 0.0883883), big)
     torch.cuda.synchronize()
+
+
+def test_graphs_captured_without_an_eager_call(llmik, cuda):
+    """Two graphs captured on a stream that never ran the ops eagerly. Each
+    capture creates its own workspace, zeroed inside that graph only, and
+    none is cached for the stream: replaying the second graph before the
+    first, then an eager call on the same stream, all match eager calls on
+    another stream bit for bit (a cached capture-time buffer would reach the
+    second graph and the eager call with counters never zeroed)."""
+    gen = torch.Generator(device=cuda).manual_seed(21)
+    q = torch.randn((2, 32, 128), generator=gen, device=cuda, dtype=torch.float16)
+    k = torch.randn((2, 8, 4096, 128), generator=gen, device=cuda, dtype=torch.float16)
+    v = torch.randn((2, 8, 4096, 128), generator=gen, device=cuda, dtype=torch.float16)
+    q2 = torch.randn((1, 32, 128), generator=gen, device=cuda, dtype=torch.float16)
+    k2 = torch.randn((1, 8, 3000, 128), generator=gen, device=cuda, dtype=torch.float16)
+    v2 = torch.randn((1, 8, 3000, 128), generator=gen, device=cuda, dtype=torch.float16)
+    act = torch.randn((1, 4096), generator=gen, device=cuda, dtype=torch.float16)
+    w = torch.randint(-2 ** 31, 2 ** 31 - 1, (512, 4096), generator=gen, device=cuda, dtype=torch.int32)
+    sc = (torch.rand((32, 4096), generator=gen, device=cuda) * 0.01).half()
+    ref1 = llmik.decode_attention(q, k, v, 0.0883883)
+    ref2 = llmik.decode_attention(q2, k2, v2, 0.0883883)
+    refw = llmik.w4a16_gemm_f32out(act, w, sc, 128)
+    torch.cuda.synchronize()
+    # torch draws streams from a pool: take one whose handle no op has used.
+    streams = [torch.cuda.Stream(device=cuda) for _ in range(40)]
+    stream = next(s for s in streams if (cuda.index or 0, s.cuda_stream) not in llmik._WORKSPACES)
+    key = (cuda.index or 0, stream.cuda_stream)
+    g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1, stream=stream):
+        o1 = llmik.decode_attention(q, k, v, 0.0883883)
+    with torch.cuda.graph(g2, stream=stream):
+        o2 = llmik.decode_attention(q2, k2, v2, 0.0883883)
+        ow_ = llmik.w4a16_gemm_f32out(act, w, sc, 128)
+    assert key not in llmik._WORKSPACES, "a capture-time workspace must not be cached"
+    for _ in range(3):
+        with torch.cuda.stream(stream):
+            g2.replay()
+        stream.synchronize()
+        assert torch.equal(o2, ref2) and torch.equal(ow_, refw)
+        with torch.cuda.stream(stream):
+            g1.replay()
+        stream.synchronize()
+        assert torch.equal(o1, ref1)
+    with torch.cuda.stream(stream):
+        e1 = llmik.decode_attention(q, k, v, 0.0883883)
+        e2 = llmik.decode_attention(q2, k2, v2, 0.0883883)
+    stream.synchronize()
+    assert torch.equal(e1, ref1) and torch.equal(e2, ref2)
+    assert key in llmik._WORKSPACES

@@ -7,9 +7,13 @@
 * round-trip bound |x - dequant(quant(x))| <= absmax/qmax
   (the reference's tests/test_kv_cache.py:57-116);
 * packing <-> unpacking inverse and the byte layout;
+* golden rows holding NaN, +-inf and fp16 overflow (reference-written):
+  torch's amax propagates NaN, so such a row stores scale NaN / +inf and
+  codes 0, in all three conventions (fp32, fp16, and fp16 input .float());
 * plant-a-mistake: oracle variants with a plausible error (reciprocal
   multiply, round-half-away, no clamp floor, fp16 scale before the
-  division for fp32 inputs) must fail the golden vectors.
+  division for fp32 inputs, a NaN-dropping absmax) must fail the golden
+  vectors.
 """
 from __future__ import annotations
 
@@ -49,6 +53,56 @@ def test_groupwise_matches_reference_golden(name, bits, gs):
     q, s = kq.quantize_per_channel_groupwise(x, bits, gs)
     assert _same_bits(q, GOLD[f"{name}_b{bits}_g{gs}_q"])
     assert _same_bits(s, GOLD[f"{name}_b{bits}_g{gs}_s"])
+
+
+def _same_bits_nan(a: np.ndarray, b: np.ndarray) -> bool:
+    """Bit-exact, except that a NaN matches any NaN: torch's own NaN payload
+    depends on its reduction path (0x7FC00000 from the per-token reduction,
+    0xFFFFFFFF from the group-axis one on this CPU), so it pins nothing."""
+    if a.dtype != b.dtype or a.shape != b.shape:
+        return False
+    na, nb = np.isnan(a), np.isnan(b)
+    return bool((na == nb).all()) and np.array_equal(a[~na].view(np.uint8), b[~nb].view(np.uint8))
+
+
+def _nonfinite_inputs(prefix: str):
+    x32 = GOLD[f"{prefix}_x32"]
+    with np.errstate(over="ignore"):
+        x16 = x32.astype(np.float16)
+    return {f"{prefix}_x32": x32, f"{prefix}_x16": x16, f"{prefix}_x16f": x16.astype(np.float32)}
+
+
+@pytest.mark.parametrize("name", ["nf_pt_x32", "nf_pt_x16", "nf_pt_x16f"])
+@pytest.mark.parametrize("bits", [8, 4])
+def test_per_token_nonfinite_rows_match_reference_golden(name, bits):
+    x = _nonfinite_inputs("nf_pt")[name]
+    q, s = kq.quantize_per_token(x, bits)
+    assert _same_bits(q, GOLD[f"{name}_b{bits}_q"])
+    assert _same_bits_nan(s, GOLD[f"{name}_b{bits}_s"])
+    # The closed form behind those bits: a NaN row -> scale NaN, an inf row
+    # (no NaN) -> scale +inf, and all codes 0 in both.
+    bad = ~np.isfinite(x).all(axis=-1)
+    assert (q[bad] == 0).all() and not np.isfinite(s[bad]).any()
+
+
+@pytest.mark.parametrize("name", ["nf_gw_x32", "nf_gw_x16", "nf_gw_x16f"])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 128])
+def test_groupwise_nonfinite_rows_match_reference_golden(name, bits, gs):
+    x = _nonfinite_inputs("nf_gw")[name]
+    q, s = kq.quantize_per_channel_groupwise(x, bits, gs)
+    assert _same_bits(q, GOLD[f"{name}_b{bits}_g{gs}_q"])
+    assert _same_bits_nan(s, GOLD[f"{name}_b{bits}_g{gs}_s"])
+    assert np.isnan(s).any() and np.isinf(s).any()
+
+
+def test_nan_dropping_absmax_fails_nonfinite_golden():
+    """Plant: an absmax that skips NaN (as fmaxf does) stores a
+    finite scale for a row holding a NaN, and the golden rows catch it."""
+    x = _nonfinite_inputs("nf_pt")["nf_pt_x16f"]
+    absmax = np.where(np.isnan(x), 0.0, np.abs(x)).max(axis=-1, keepdims=True)
+    s = np.maximum(absmax / np.float32(127), np.float32(1e-8))
+    assert not _same_bits_nan(s[..., 0], GOLD["nf_pt_x16f_b8_s"])
 
 
 def test_half_even_ties_by_hand():

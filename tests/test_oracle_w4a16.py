@@ -56,6 +56,22 @@ def test_quantizer_matches_reference_golden(name, gs):
         assert np.array_equal(ow.pack_int4_along_k(q), GOLD[f"{name}_g{gs}_packed"])
 
 
+@pytest.mark.parametrize("name", ["Wn32", "Wn16"])
+@pytest.mark.parametrize("gs", [64, 128])
+def test_quantizer_nonfinite_matches_reference_golden(name, gs):
+    """Weights holding NaN, +-inf and fp16 overflow: a group column with a
+    NaN stores scale NaN, one with an inf (no NaN) +inf, and codes 0."""
+    with np.errstate(invalid="ignore"):
+        q, s = ow.quantize_weights_int4_groupwise(GOLD[name], gs)
+    g = GOLD[f"{name}_g{gs}_s"]
+    assert np.array_equal(q, GOLD[f"{name}_g{gs}_q"])
+    # NaN matches any NaN (torch's payload depends on its reduction path).
+    assert s.dtype == g.dtype and np.array_equal(np.isnan(s), np.isnan(g))
+    assert np.array_equal(s[~np.isnan(s)].view(np.uint8), g[~np.isnan(g)].view(np.uint8))
+    assert np.array_equal(ow.pack_int4_along_k(q), GOLD[f"{name}_g{gs}_packed"])
+    assert np.isnan(s.astype(np.float32)).any() and np.isinf(s.astype(np.float32)).any()
+
+
 def test_fp16_and_fp32_weight_conventions_differ():
     # For fp16 W the scale is rounded before the division; the codes of the
     # two conventions must not be assumed equal.
