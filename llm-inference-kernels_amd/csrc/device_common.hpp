@@ -249,10 +249,15 @@ __device__ __forceinline__ float sym_scale(uint32_t absmax_bits, float qmax) {
 // clamp(round(x / s), -qmax, qmax) as an integer code (r = 1 / s). A NaN
 // quotient (a NaN scale, or inf / inf) gives code 0, which is what torch's
 // float -> int8 conversion of NaN stores on x86; finite / inf is 0 already.
-__device__ __forceinline__ int sym_code(float x, float s, float r, float qmax) {
+// v_cvt_i32_f32 converts NaN to 0 and saturates out-of-range values (CDNA
+// ISA), so the conversion comes first and the clamp is one integer med3; it
+// is written as inline asm because a C++ float -> int conversion of NaN is
+// undefined behaviour the compiler may exploit.
+__device__ __forceinline__ int sym_code(float x, float s, float r, int qmax) {
     const float v = quant_round(x, s, r);
-    if (v != v) return 0;
-    return (int)fminf(fmaxf(v, -qmax), qmax);
+    int c;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(c) : "v"(v));
+    return min(max(c, -qmax), qmax);
 }
 
 }  // namespace llmik

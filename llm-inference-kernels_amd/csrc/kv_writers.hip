@@ -83,7 +83,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
         const float rcp = 1.0f / sc;
         int code[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) code[e] = sym_code(xf[e], sc, rcp, (float)QMAX);
+        for (int e = 0; e < 8; ++e) code[e] = sym_code(xf[e], sc, rcp, QMAX);
         if (flat < rows) {
             const long row = MAPPED ? map.dst((uint32_t)flat) : flat;
             if constexpr (PACK4) {
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
         f16x8_to_f32(raw[i], xf);
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7.0f) & 0xF) << (4 * e);
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7) & 0xF) << (4 * e);
         if (t < t_end)
             __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(q + (qbase + t) * 64 + 4 * c));
     }
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_larg
         f16x8_to_f32(load16(x + (base + t) * 128 + 8 * c), xf);
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7.0f) & 0xF) << (4 * e);
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7) & 0xF) << (4 * e);
         *reinterpret_cast<uint32_t*>(q + (qbase + t) * 64 + 4 * c) = w;
     }
 }
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
         f16x8_to_f32(raw[i], xf);
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7.0f) & 0xF) << (4 * e);
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sv[e], rcp[e], 7) & 0xF) << (4 * e);
         if (t <= r) *reinterpret_cast<uint32_t*>(k_q + (bh * max_len + start + t) * 64 + 4 * c) = w;
     }
 
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
         const float rc = 1.0f / sc;
         uint32_t w = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sc, rc, 7.0f) & 0xF) << (4 * e);
+        for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sc, rc, 7) & 0xF) << (4 * e);
         *reinterpret_cast<uint32_t*>(v_q + (bh * max_len + pos) * 64 + 4 * c) = w;
         if (c == 0) v_scale[bh * max_len + pos] = f2h_bits(sc);
     }
