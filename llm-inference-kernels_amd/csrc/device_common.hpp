@@ -210,19 +210,22 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c1, float s1
 // ---- exact symmetric quantisation step ------------------------------------
 // Returns rint(x / s) with x / s the IEEE correctly rounded fp32 quotient,
 // which is what torch's CPU `x / scale` followed by `.round()` computes.
-// `r` must be the fp32 reciprocal of s. The product x*r is within ~2 ulp of
-// x/s, so it only decides the rounding when it is clear of a half-integer;
-// near a half-integer (where a 2-ulp error could flip the result, or where
-// the exact quotient is a tie that rounds to even) the true division runs.
+// `r` must be within 1 ulp of 1 / s (v_rcp_f32, recip_approx below, is).
+// For |x / s| <= 256 the product y = x * r is then within 2^-14 of the
+// correctly rounded quotient (256 * (2^-23 + 2^-24 + 2^-24)), so both round
+// to the same integer unless y lies that close to a half-integer; within
+// 2^-12 of one (a tie of the true quotient rounds to even, a near-tie may go
+// either way) the true division runs. NaN and infinite quotients come out
+// of the fast path unchanged.
 __device__ __forceinline__ float quant_round(float x, float s, float r) {
     const float y = x * r;
     const float k = __builtin_rintf(y);
-    const float frac = fabsf(y - k);
-    if (fabsf(frac - 0.5f) <= 1.0e-4f * fmaxf(1.0f, fabsf(y))) {
-        return __builtin_rintf(x / s);
-    }
+    if (fabsf(fabsf(y - k) - 0.5f) <= 0x1p-12f) return __builtin_rintf(x / s);
     return k;
 }
+
+// 1 / s to within 1 ulp (v_rcp_f32): the reciprocal quant_round expects.
+__device__ __forceinline__ float recip_approx(float s) { return __builtin_amdgcn_rcpf(s); }
 
 // ---- torch's non-finite semantics for the symmetric quantisers ------------
 // |x| as bits. With the sign cleared, the unsigned order of the bit patterns

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
         amax = row16_umax(amax);
 
         const float sc = sym_scale(amax, (float)QMAX);
-        const float rcp = 1.0f / sc;
+        const float rcp = recip_approx(sc);
         int code[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) code[e] = sym_code(xf[e], sc, rcp, QMAX);
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_kern
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         sv[e] = s_scale[8 * c + e];
-        rcp[e] = 1.0f / sv[e];
+        rcp[e] = recip_approx(sv[e]);
     }
 #pragma unroll
     for (int i = 0; i < TPR; ++i) {
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kWriterThreads) void quantize_k_groupwise_int4_larg
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         sv[e] = s_scale[8 * c + e];
-        rcp[e] = 1.0f / sv[e];
+        rcp[e] = recip_approx(sv[e]);
     }
     for (int t = t_start + row; t < t_end; t += 16) {
         float xf[8];
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         sv[e] = s_scale[8 * c + e];
-        rcp[e] = 1.0f / sv[e];
+        rcp[e] = recip_approx(sv[e]);
     }
 #pragma unroll
     for (int i = 0; i < TPR; ++i) {
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kWriterThreads) void kivi_append_token_kernel(
         for (int e = 0; e < 8; ++e) amax1 = max(amax1, abs_bits(xf[e]));
         amax1 = row16_umax(amax1);
         const float sc = sym_scale(amax1, 7.0f);
-        const float rc = 1.0f / sc;
+        const float rc = recip_approx(sc);
         uint32_t w = 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) w |= (uint32_t)(sym_code(xf[e], sc, rc, 7) & 0xF) << (4 * e);

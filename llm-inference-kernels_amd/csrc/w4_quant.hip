@@ -10,9 +10,10 @@
 // dtype semantics, as torch evaluates them:
 //   * fp16 W: absmax / 7 is an fp32 quotient rounded to fp16, and the 1e-8
 //     floor is fp16(1e-8) = 0; fp32 W: fp32 quotient, floor 1e-8f;
-//   * the code division is IEEE fp32 division (correctly rounded), rint is
-//     round-half-to-even, and a NaN quotient (0 / 0 of an all-zero fp16
-//     group) becomes code 0;
+//   * the code is rint of the IEEE fp32 quotient (correctly rounded; formed
+//     as x * (1 / s) with the true division near half-integers, quant_round),
+//     rint is round-half-to-even, and a NaN quotient (0 / 0 of an all-zero
+//     fp16 group) becomes code 0;
 //   * a short last group (K % g != 0) uses only its real rows: the
 //     reference's zero padding never raises an absmax.
 // With group_size % 8 == 0 (up to 1024) and K % 8 == 0 one workgroup codes
@@ -70,9 +71,10 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_w4_kernel(
     if (scale_f16) scale_f16[(long)g * N + n] = s16;
 
     uint32_t word = 0;
+    const float r = recip_approx(s);
     for (int k = k0; k < k1; ++k) {
         const float x = w_at<F16>(W, (long)k * N + n);
-        float c = __builtin_rintf(x / s);
+        float c = quant_round(x, s, r);
         if (c != c) c = 0.0f;   // a NaN quotient (0 / 0, or a NaN weight or scale) -> code 0
         c = fminf(fmaxf(c, -7.0f), 7.0f);
         const int code = (int)c;
@@ -152,6 +154,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void quantize_w4_tile_kernel(
         }
         if (scale_f16) scale_f16[(long)g * N + n] = s16;
     }
+    const float r = recip_approx(s);
 #pragma unroll
     for (int j = 0; j < SP; ++j) {
         const int sl = wave + kTileWaves * j;
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void quantize_w4_tile_kernel(
         uint32_t word = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            float c = __builtin_rintf(x[j][i] / s);
+            float c = quant_round(x[j][i], s, r);
             if (c != c) c = 0.0f;   // a NaN quotient -> code 0
             c = fminf(fmaxf(c, -7.0f), 7.0f);
             const int code = (int)c;
