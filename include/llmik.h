@@ -319,6 +319,16 @@ LLMIK_API llmik_status llmik_w4a16_gemm_qkv_rope_f16(
 LLMIK_API void llmik_w4a16_set_plan_override(int stream_mode, int stream_splits);
 
 /*
+ * Plan knob of the fp16 attention entry points, for measurement and tests (no
+ * reference counterpart). f16_half_tiles: 1 runs every fp16 call on the MFMA
+ * path with 16-token tiles, 0 with 32-token tiles, -1 restores the rule (16-
+ * token tiles for at least 32 (batch, kv head, head chunk) slabs and 2-8
+ * 32-token tiles per wave). Not synchronised with calls in flight on other
+ * threads.
+ */
+LLMIK_API void llmik_attention_set_plan_override(int f16_half_tiles);
+
+/*
  * Materialise fp16 W[k, n] = fp16(q[k, n] * scale[k/g, n]).
  * Replaces: w4a16_dequantize op (bindings/extension.cpp:382-403) and
  *   launch_w4a16_dequantize (kernels/quant/quant_matmul.cuh:58-60;

@@ -47,6 +47,8 @@
 //   I4 : k,v [B,Hkv,L,64] packed int4 (even channel in the low nibble),
 //        k_scale [B,Hkv,n_groups,128] fp16 (per channel, per group of
 //        group_size tokens), v_scale [B,Hkv,L] fp16 (per token)
+#include <atomic>
+
 #include "device_common.hpp"
 #include "llmik_internal.hpp"
 
@@ -751,6 +753,169 @@ void decode_attention_mfma_kernel(AttnParams p) {
 }
 
 // ===========================================================================
+// fp16, 16-token tiles with the next tile in flight
+// ===========================================================================
+// The kernel above issues a whole 16 KiB fp16 tile per wave and waits for
+// it; here a wave walks 16-token tiles (4 KiB of K, 4 KiB of V), the split's
+// tiles interleaved as above at 16-token granularity (split s, wave w reads
+// tiles s + n_splits * (w + NW * i)), with the next tile's loads issued
+// before the current tile's arithmetic: the same 16 KiB per wave stays in
+// flight, in two staggered halves, and a wave's reads end in 8 KiB steps
+// instead of 16 KiB ones, which evens out when the waves of the grid finish.
+// QK is one 16-token block; PV runs v_mfma_f32_16x16x16_f16 over the tile's
+// 16 tokens (hi and lo P planes against the same B operand).
+// launch_attention picks it for fp16 where it measured faster (see
+// use_f16_half_tiles).
+constexpr int kHalfTile = 16;
+
+struct F16HalfTile {
+    static constexpr uint32_t kRow = kHeadDim * 2;
+    u32x4 k[4];   // lane (g, c): token c, channels 32 ks + 8 g
+    u32x4 v[4];   // lane (g, c): token 4 g + e, channels 8 c
+    __device__ __forceinline__ void load(const TileCtx& x, int t0) {
+        const uint32_t so = (uint32_t)t0 * kRow;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            k[ks] = __builtin_amdgcn_raw_buffer_load_b128(x.rk, (int)x.koff, (int)(so + 64 * ks), 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[e] = __builtin_amdgcn_raw_buffer_load_b128(x.rv, (int)x.voff, (int)(so + kRow * e), 2);
+    }
+    // B operand of PV MFMA j (channels 8 c + j): V[4 g + e][8 c + j], e = 0..3.
+    __device__ __forceinline__ f16x4 vop(int j) const {
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t d0 = perm_b32(v[1][j >> 1], v[0][j >> 1], sel);
+        const uint32_t d1 = perm_b32(v[3][j >> 1], v[2][j >> 1], sel);
+        return __builtin_bit_cast(f16x4, u32x2{d0, d1});
+    }
+};
+
+template <int HPW, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_attention_f16h_kernel(AttnParams p) {
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y / p.n_hchunks;
+    const int hchunk = blockIdx.y % p.n_hchunks;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int head0 = kvh * p.gqa + hchunk * HPW;
+    const uint16_t* qrow = p.q + ((long)b * p.n_heads + head0 + ((c >> 2) % HPW)) * kHeadDim;
+    f16x8 qa[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qa[ks] = as_f16x8(load16(qrow + 32 * ks + 8 * g));
+    f32x4 o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][2][4][kHalfTile];
+    __shared__ __attribute__((aligned(16))) float s_alpha[NW][4];
+
+    const int w0 = (split + p.n_splits * wave) * kHalfTile;
+    const int w1 = p.seqlen;
+    const int stride = p.n_splits * NW * kHalfTile;
+    TileCtx x;
+    {
+        const long slab = (long)(b * p.n_kv_heads + kvh);
+        constexpr uint32_t kRow = F16HalfTile::kRow;
+        const long kv_base = slab * p.kv_buf_len * (long)kRow;
+        const uint32_t range = (uint32_t)max(w1, 0) * kRow;
+        x.rk = make_buffer_rsrc(static_cast<const char*>(p.k) + kv_base, range);
+        x.rv = make_buffer_rsrc(static_cast<const char*>(p.v) + kv_base, range);
+        x.koff = (uint32_t)c * kRow + 16u * g;
+        x.voff = 4u * g * kRow + 16u * c;
+    }
+
+    auto step = [&](const F16HalfTile& tile, const int t0) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(qa[ks], as_f16x8(tile.k[ks]), acc);
+        const float s = (t0 + c) < w1 ? acc[0] * p.scale_log2 : -INFINITY;
+        const float tmax = row16_max(s);
+        const float mn = fmaxf(m_run, tmax);
+        const float msafe = (mn == -INFINITY) ? 0.0f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - msafe);
+        const bool rescale = __builtin_amdgcn_ballot_w64(mn != m_run) != 0;
+        m_run = mn;
+        const float pr = __builtin_amdgcn_exp2f(s - msafe);
+        l_run = fmaf(l_run, alpha, pr);
+        if (g < HPW) {
+            const float xv = pr * MfmaTile<KvFormat::F16>::kPScale;
+            const uint16_t h = f2h_bits(xv);
+            s_p[wave][0][g][c] = h;
+            s_p[wave][1][g][c] = f2h_bits(xv - h2f(h));
+            if (c == 0) s_alpha[wave][g] = alpha;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // A operand of PV: row c (head c % HPW), tokens 4 g .. 4 g + 3.
+        const f16x4 pa = __builtin_bit_cast(f16x4, *reinterpret_cast<const u32x2*>(&s_p[wave][0][c % HPW][4 * g]));
+        const f16x4 pl = __builtin_bit_cast(f16x4, *reinterpret_cast<const u32x2*>(&s_p[wave][1][c % HPW][4 * g]));
+        if (rescale) {
+            const f32x4 al = *reinterpret_cast<const f32x4*>(&s_alpha[wave][0]);
+            float a4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a4[i] = al[i % HPW];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[j][i] *= a4[i];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const f16x4 vb = tile.vop(j);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, o[j], 0, 0, 0);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, o[j], 0, 0, 0);
+        }
+    };
+
+    if (w0 < w1) {
+        // The prefetch past the range reads zeros through the buffer bound;
+        // it is unconditional so that the wait counts stay exact.
+        F16HalfTile ta, tb;
+        int t0 = w0;
+        ta.load(x, t0);
+        while (true) {
+            tb.load(x, t0 + stride);
+            __builtin_amdgcn_sched_barrier(0);
+            step(ta, t0);
+            t0 += stride;
+            if (t0 >= w1) break;
+            ta.load(x, t0 + stride);
+            __builtin_amdgcn_sched_barrier(0);
+            step(tb, t0);
+            t0 += stride;
+            if (t0 >= w1) break;
+        }
+    }
+
+    const float l_tot = row16_sum(l_run);
+    __shared__ __attribute__((aligned(16))) float s_o[NW][HPW][kHeadDim];
+    __shared__ float s_m[NW][HPW];
+    __shared__ float s_l[NW][HPW];
+    __shared__ uint32_t s_last;
+    constexpr float kInvP = 1.0f / MfmaTile<KvFormat::F16>::kPScale;
+    if (g == 0) {
+#pragma unroll
+        for (int i = 0; i < HPW; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s_o[wave][i][8 * c + j] = o[j][i] * kInvP;
+    }
+    if (c == 0 && g < HPW) {
+        s_m[wave][g] = m_run;
+        s_l[wave][g] = l_tot;
+    }
+    __syncthreads();
+    finish_split<NW, HPW, NW * kWave>(p, s_o, s_m, s_l, &s_last, b, kvh, hchunk, split, head0);
+}
+
+// ===========================================================================
 // VALU fallback kernel
 // ===========================================================================
 
@@ -1002,8 +1167,40 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
     return pl;
 }
 
+// fp16 16-token tiles (decode_attention_f16h_kernel) against 32-token ones,
+// on one box (us, 32 -> 16): B=4 S=4096 16.06 -> 15.33, B=8 S=2048 15.59 ->
+// 15.21, B=8 S=4096 26.26 -> 25.05, B=8 S=8192 46.03 -> 45.48, B=16 S=4096
+// 46.11 -> 43.47, B=4 S=8192 26.50 -> 26.11; slower with one tile per wave
+// (B=4 S=2048 10.54 -> 11.47, B=2 S=4096 11.79 -> 12.21, B=8 S=1024) and
+// with 16 (B=8 S=16384 84.8 -> 87.3); about even at B=1-2 S=8192-16384 with
+// fewer than 32 workgroups per split, B=16 S=2048, B=32-64. The rule: at
+// least 32 (batch, kv head, head chunk) slabs and 2-8 32-token tiles per
+// wave. The override (llmik_attention_set_plan_override) forces either.
+namespace {
+std::atomic<int> g_f16_tiles{-1};   // -1: the rule, 0: 32-token tiles, 1: 16-token tiles
+}  // namespace
+
+void set_attention_plan_override(int f16_half_tiles) {
+    g_f16_tiles.store(f16_half_tiles < 0 ? -1 : (f16_half_tiles ? 1 : 0), std::memory_order_relaxed);
+}
+
+static bool use_f16_half_tiles(const AttnPlan& pl, int seqlen) {
+    const int mode = g_f16_tiles.load(std::memory_order_relaxed);
+    if (mode >= 0) return mode == 1;
+    const long tiles = (seqlen + kTile - 1) / kTile;
+    const long per_wave = (tiles + (long)pl.n_splits * pl.waves - 1) / ((long)pl.n_splits * pl.waves);
+    return pl.n_slot_groups >= 32 && per_wave >= 2 && per_wave <= 8;
+}
+
 template <KvFormat F, int HPW>
-static void launch_kernel(const AttnParams& p, dim3 grid, bool mfma, int waves, hipStream_t stream) {
+static void launch_kernel(const AttnParams& p, dim3 grid, bool mfma, int waves, bool half, hipStream_t stream) {
+    if (F == KvFormat::F16 && mfma && half) {
+        if (waves == 8)
+            hipLaunchKernelGGL((decode_attention_f16h_kernel<HPW, 8>), grid, dim3(8 * kWave), 0, stream, p);
+        else
+            hipLaunchKernelGGL((decode_attention_f16h_kernel<HPW, 4>), grid, dim3(4 * kWave), 0, stream, p);
+        return;
+    }
     if (mfma && waves == 8) {
         hipLaunchKernelGGL((decode_attention_mfma_kernel<F, HPW, 8>), grid, dim3(8 * kWave), 0,
                            stream, p);
@@ -1050,11 +1247,12 @@ static int launch_attention(const AttnLaunch& a, hipStream_t stream) {
     const long row_bytes = (F == KvFormat::F16) ? 2 * kHeadDim : (F == KvFormat::I8 ? kHeadDim : kHeadDim / 2);
     const bool mfma = ((F != KvFormat::I4) || (p.group_size % kTile == 0)) &&
                       (long)a.kv_buf_len * row_bytes < (1L << 32);
+    const bool half = (F == KvFormat::F16) && mfma && use_f16_half_tiles(pl, a.seqlen);
     dim3 grid(pl.n_splits, a.n_kv_heads * pl.n_hchunks, a.batch);
     switch (pl.hpw) {
-        case 4: launch_kernel<F, 4>(p, grid, mfma, pl.waves, stream); break;
-        case 2: launch_kernel<F, 2>(p, grid, mfma, pl.waves, stream); break;
-        default: launch_kernel<F, 1>(p, grid, mfma, pl.waves, stream); break;
+        case 4: launch_kernel<F, 4>(p, grid, mfma, pl.waves, half, stream); break;
+        case 2: launch_kernel<F, 2>(p, grid, mfma, pl.waves, half, stream); break;
+        default: launch_kernel<F, 1>(p, grid, mfma, pl.waves, half, stream); break;
     }
     return check_launch();
 }

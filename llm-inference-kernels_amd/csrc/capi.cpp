@@ -374,6 +374,10 @@ LLMIK_API void llmik_w4a16_set_plan_override(int stream_mode, int stream_splits)
     set_w4a16_plan_override(stream_mode, stream_splits);
 }
 
+LLMIK_API void llmik_attention_set_plan_override(int f16_half_tiles) {
+    set_attention_plan_override(f16_half_tiles);
+}
+
 LLMIK_API llmik_status llmik_w4a16_dequantize(const void* weight_packed, const void* scale,
                                               void* out, int K, int N, int group_size,
                                               void* stream) {

@@ -39,6 +39,8 @@ struct AttnPlan {
 };
 
 AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen);
+// fp16 tile size knob (see llmik_attention_set_plan_override).
+void set_attention_plan_override(int f16_half_tiles);
 // W4A16 plan knobs (see llmik_w4a16_set_plan_override).
 void set_w4a16_plan_override(int stream_mode, int stream_splits);
 

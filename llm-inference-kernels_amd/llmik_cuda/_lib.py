@@ -54,6 +54,7 @@ _SIGNATURES = {
     "llmik_w4a16_gemm_f32out": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
     "llmik_w4a16_dequantize": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "llmik_w4a16_set_plan_override": (None, [_i, _i]),
+    "llmik_attention_set_plan_override": (None, [_i]),
     "llmik_w4a16_swiglu_workspace_size": (_sz, [_i, _i, _i, _i]),
     "llmik_w4a16_gemm_swiglu": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
     "llmik_w4a16_qkv_rope_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
