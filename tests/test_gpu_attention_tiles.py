@@ -84,7 +84,8 @@ def test_fp16_tile_forms_match_oracle(llmik, cuda, B, H, Hkv, S, buf, rule_half)
     for mode in (0, 1):
         err = float(np.abs(outs[mode][rows].double().cpu().numpy() - ref).max())
         assert err <= TOL, f"form {'16' if mode else '32'}-token: {err}"
-    assert torch.equal(outs[-1], outs[1 if rule_half else 0])
+    if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:   # the plans named above
+        assert torch.equal(outs[-1], outs[1 if rule_half else 0])
 
 
 @pytest.mark.parametrize("B,S", [(8, 4096), (4, 8191)])
