@@ -55,6 +55,7 @@ CASES = [
     (2, 32, 8, 4096, 4096, False),    # 16 slabs
     (8, 32, 8, 1024, 1024, False),    # 4-wave workgroups, 1 tile per wave
     (4, 64, 8, 2000, 2000, True),     # GQA 8: two head chunks per kv head
+    (8, 24, 8, 2000, 2000, True),     # GQA 3: one head per workgroup, three chunks per kv head
 ]
 
 
