@@ -37,6 +37,9 @@
 //   fp16 hi + lo pair in alternate rows of QK's A operand, so the product
 //   keeps fp32 precision at one MFMA per k-step; INT4's PV likewise carries
 //   both P planes in one MFMA, in alternate lane groups' rows).
+// fp16 16-token form (decode_attention_f16h_kernel): the same products over
+// 16-token tiles with the next tile's loads in flight (PV on
+// v_mfma_f32_16x16x16_f16), for the plans where it measured faster.
 // Fallback kernel (decode_attention_valu_kernel): fp32 VALU with 16-lane
 // DPP reductions; used for INT4 group sizes that are not multiples of 32.
 //
