@@ -8,7 +8,8 @@ of 1-2000 tokens with the live length anywhere in them (or the whole
 buffer), INT4 groups of 16, 32, 48, 64 and 128 tokens (16 and 48 run the
 VALU kernel). These reach split counts from 1 to 8, 4- and 8-wave
 workgroups, one, two and four query heads per workgroup, partial last
-tiles and partial last INT4 groups.
+tiles and partial last INT4 groups. The fp16 shapes run a second time with
+every call forced onto the 16-token-tile kernel.
 """
 from __future__ import annotations
 
@@ -76,4 +77,28 @@ def test_random_shapes_match_oracle(llmik, cuda, fmt, B, H, Hkv, L, live, gs, se
         v_ref = kq.dequantize_per_token(kq.unpack_kv_int4(vq_.cpu().numpy()), vs.cpu().numpy())
     ref = oa.decode_attention(q, k_ref, v_ref, scale, seqlen=None if live < 0 else live)
     assert out.shape == (B, H, 128) and out.dtype == torch.float16
+    assert float(np.abs(out.float().cpu().numpy() - ref).max()) <= TOL
+
+
+FP16_CONFIGS = [c for c in CONFIGS if c[0] == "fp16"]
+
+
+@pytest.mark.parametrize("fmt,B,H,Hkv,L,live,gs,seed", FP16_CONFIGS,
+                         ids=[f"half-B{c[1]}-H{c[2]}-Hkv{c[3]}-L{c[4]}-live{c[5]}" for c in FP16_CONFIGS])
+def test_random_shapes_fp16_half_tiles(llmik, cuda, fmt, B, H, Hkv, L, live, gs, seed):
+    """The same fp16 shapes with every call forced onto the 16-token-tile
+    kernel (llmik_attention_set_plan_override(1)), which the planner picks
+    only for larger batches."""
+    from llmik_cuda._lib import lib
+    q = randn((B, H, 128), seed).astype(np.float16)
+    k = randn((B, Hkv, L, 128), seed + 1).astype(np.float16)
+    v = randn((B, Hkv, L, 128), seed + 2).astype(np.float16)
+    scale = 1.0 / math.sqrt(128)
+    lib.llmik_attention_set_plan_override(1)
+    try:
+        out = llmik.decode_attention(_dev(q, cuda), _dev(k, cuda), _dev(v, cuda), scale, live)
+        torch.cuda.synchronize()
+    finally:
+        lib.llmik_attention_set_plan_override(-1)
+    ref = oa.decode_attention(q, k, v, scale, seqlen=None if live < 0 else live)
     assert float(np.abs(out.float().cpu().numpy() - ref).max()) <= TOL
