@@ -689,11 +689,31 @@ void decode_attention_mfma_kernel(AttnParams p) {
         // One 16 / 8 KiB fp16 / INT8 tile per wave in flight already keeps
         // 32 / 16 MiB of loads queued chip-wide; a second one only lengthens
         // the queue (measured slower for both).
+        //
+        // INT8 with splits: KV head h starts its walk h / Hkv of the way into
+        // the sequence and wraps (tile t reads tile (t + rot) mod n_tiles),
+        // so the heads of a batch row do not all read the same relative
+        // position of their K and V at once. The rotation depends on the
+        // head alone, so a batch permutation still permutes the outputs bit
+        // for bit. Against the unrotated walk on four boxes (us): B=4
+        // S=4096 11.6-12.0 -> 10.6 on every box, A8 15.5-16.1 -> 15.4-15.7,
+        // B=16 26.2-29.2 -> 26.1-28.9, B=8 S=1024 +1 %, and B=8 S=16384
+        // either way with the box (49-59 -> 46.8, 51.8 -> 55.0); without
+        // splits (B=64) it was 2.5 % slower, so unsplit plans keep the plain
+        // walk.
+        // fp16 is not rotated: B=8 S=8192 53-63 -> 46-49 us, but the A16
+        // headline 25.1-25.3 -> 25.5-28.0 and B=64 +1.3 %.
+        const int n_rt = (w1 + kTile - 1) / kTile;
+        const int rot = (F == KvFormat::I8 && p.n_splits > 1)
+            ? (int)((long)kvh * n_rt / p.n_kv_heads) * kTile : 0;
+        const int n_tok = n_rt * kTile;
         for (int t0 = w0; t0 < w1; t0 += p.n_splits * NW * kTile) {
             MfmaTile<F> tile;
-            load_tile(tile, t0);
+            int tp = t0 + rot;
+            if (tp >= n_tok) tp -= n_tok;
+            load_tile(tile, tp);
             __builtin_amdgcn_sched_barrier(0);
-            step(tile, t0);
+            step(tile, tp);
         }
     } else if (w0 < w1) {
         // INT4 tiles are 4 KiB per wave: the next tile's loads are issued

@@ -115,6 +115,47 @@ def test_int8_live_length(llmik, cuda):
     assert _max_abs(out, oa.decode_attention(q, k_dq, v_dq, 0.0883883, seqlen=700)) <= TOL
 
 
+@pytest.mark.parametrize("B,L,live", [(8, 4096, 4096), (4, 4097, 4097), (8, 3500, 3001), (32, 1500, 1500),
+                                      (2, 16384, 16383)])
+def test_int8_rotated_walk(llmik, cuda, B, L, live):
+    """Under a split plan, INT8 KV head h walks its tiles starting h / Hkv
+    of the way into the sequence and wraps. Cases: the A8 config; a
+    one-token last tile that the rotation places mid-walk (4097); a live
+    length inside a longer buffer whose tail codes and scales are poisoned
+    (3001 of 3500); 4-wave workgroups and no split, the plain walk (B=32,
+    S=1500); 16 splits (B=2) and a live length one short of the buffer
+    (16383 of 16384).
+    Oracle parity (float64) on sampled rows, bit-equal repeats, and a batch
+    permutation that permutes the outputs bit for bit."""
+    gen = torch.Generator(device=cuda).manual_seed(B * 13 + L)
+    kd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    kd[..., [7, 77]] *= 12
+    vd = torch.randn((B, 8, L, 128), generator=gen, device=cuda, dtype=torch.float16)
+    kq_, ks = llmik.quantize_per_token(kd)
+    vq_, vs = llmik.quantize_per_token(vd)
+    del kd, vd
+    if live < L:
+        kq_[:, :, live:] = 127
+        vq_[:, :, live:] = -127
+        ks[:, :, live:] = float("nan")
+        vs[:, :, live:] = float("inf")
+    q = randn((B, 32, 128), B * 17 + L).astype(np.float16)
+    qd = _dev(q, cuda)
+    scale = 1 / math.sqrt(128)
+    out = llmik.decode_attention_int8(qd, kq_, ks, vq_, vs, scale, seqlen=live)
+    rows = sorted({0, B // 2, B - 1})
+    _sampled_rows_parity(
+        out, q,
+        lambda b: kq.dequantize_per_token(kq_[b:b + 1, :, :live].cpu().numpy(), ks[b:b + 1, :, :live].cpu().numpy()),
+        lambda b: kq.dequantize_per_token(vq_[b:b + 1, :, :live].cpu().numpy(), vs[b:b + 1, :, :live].cpu().numpy()),
+        rows, scale)
+    assert torch.equal(llmik.decode_attention_int8(qd, kq_, ks, vq_, vs, scale, seqlen=live), out)
+    perm = torch.randperm(B, generator=torch.Generator().manual_seed(2)).to(cuda)
+    out_p = llmik.decode_attention_int8(qd[perm].contiguous(), kq_[perm].contiguous(), ks[perm].contiguous(),
+                                        vq_[perm].contiguous(), vs[perm].contiguous(), scale, seqlen=live)
+    assert torch.equal(out_p, out[perm])
+
+
 @pytest.mark.parametrize("B,L,gs", [(1, 128, 32), (4, 1000, 32), (8, 4096, 128), (2, 100, 128),
                                     (8, 2048, 32), (1, 300, 64),
                                     # groups that are not multiples of 32: the VALU kernel
