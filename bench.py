@@ -705,7 +705,8 @@ FLOOR_RW_LOADS = (4, 8)
 def bench_floors(steps: int, warmup: int) -> list:
     """What one launch costs before it does any work, and what the plainest
     read of a product kernel's bytes costs (llmik_diag_empty /
-    llmik_diag_read, csrc/diag.hip), timed like every other row: graph
+    llmik_diag_read of libllmik_diag.so, csrc_diag/diag.hip), timed like
+    every other row: graph
     replay of `steps` calls over rotating windows of one buffer (>= 768 MiB
     in all). Each read size runs at every grid in FLOOR_GRIDS (workgroups of
     8 waves) and every depth in FLOOR_LOADS (16-byte loads per lane in
@@ -714,7 +715,9 @@ def bench_floors(steps: int, warmup: int) -> list:
     (time_steps' untimed calls, then the timed replay of "reps" calls, which
     are the row's last). A last row per size names the fastest read."""
     import torch
-    from llmik_cuda._lib import check, lib
+    from llmik_cuda._lib import diag_check as check
+    from llmik_cuda._lib import diag_lib
+    lib = diag_lib()
     dev = torch.device("cuda:0")
     rows = []
 
@@ -915,7 +918,7 @@ def main() -> None:
     ap.add_argument("--only", default="",
                     help="comma list: int8,int4,w4a16,prefill,layer,writers,append,sweep,wquant")
     ap.add_argument("--floors", action="store_true",
-                    help="time the empty-kernel and plain-read floors (csrc/diag.hip), print one "
+                    help="time the empty-kernel and plain-read floors (csrc_diag/diag.hip), print one "
                          "JSON line per row and exit")
     ap.add_argument("--pmc-workload", nargs="?", const="attn:fp16", default=None,
                     choices=PMC_WORKLOADS,

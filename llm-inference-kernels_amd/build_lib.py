@@ -5,6 +5,8 @@ Usage: python llm-inference-kernels_amd/build_lib.py [--jobs N]
 Every translation unit under csrc/ is compiled for gfx950 only, without
 fast-math (the KV writers must divide exactly), and linked into
 llmik_cuda/libllmik_hip.so next to the Python package that loads it.
+The measurement floors (csrc_diag/, include/llmik_diag.h) are linked into
+llmik_cuda/libllmik_diag.so, a library of their own.
 """
 from __future__ import annotations
 
@@ -18,8 +20,10 @@ from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent
 CSRC = PKG_ROOT / "csrc"
+CSRC_DIAG = PKG_ROOT / "csrc_diag"
 OUT_DIR = PKG_ROOT / "llmik_cuda"
 LIB_NAME = "libllmik_hip.so"
+DIAG_LIB_NAME = "libllmik_diag.so"
 OBJ_DIR = PKG_ROOT / "_build"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -38,12 +42,12 @@ COMMON_FLAGS = [
 ]
 
 
-def sources() -> list[Path]:
-    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+def sources(d: Path = CSRC) -> list[Path]:
+    return sorted(list(d.glob("*.hip")) + list(d.glob("*.cpp")))
 
 
 def compile_one(src: Path) -> Path:
-    obj = OBJ_DIR / (src.stem + ".o")
+    obj = OBJ_DIR / (src.parent.name + "_" + src.stem + ".o")
     cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -56,14 +60,7 @@ def compile_one(src: Path) -> Path:
     return obj
 
 
-def build(jobs: int = 8) -> Path:
-    if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
-        raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
-    OBJ_DIR.mkdir(exist_ok=True)
-    srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
-        objs = list(ex.map(compile_one, srcs))
-    out = OUT_DIR / LIB_NAME
+def _link(objs: list[Path], out: Path) -> Path:
     tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -71,6 +68,20 @@ def build(jobs: int = 8) -> Path:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, out)
     return out
+
+
+def build(jobs: int = 8) -> Path:
+    """Build libllmik_hip.so and, beside it, libllmik_diag.so; returns the
+    path of the product library."""
+    if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
+        raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
+    OBJ_DIR.mkdir(exist_ok=True)
+    srcs = sources()
+    diag_srcs = sources(CSRC_DIAG)
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs) + len(diag_srcs)))) as ex:
+        objs = list(ex.map(compile_one, srcs + diag_srcs))
+    _link(objs[len(srcs):], OUT_DIR / DIAG_LIB_NAME)
+    return _link(objs[:len(srcs)], OUT_DIR / LIB_NAME)
 
 
 TORCH_SRC = PKG_ROOT / "csrc_torch" / "torch_ops.cpp"

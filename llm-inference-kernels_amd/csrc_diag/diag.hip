@@ -1,6 +1,8 @@
 // Measurement kernels: the floors that the product kernels' rooflines are
 // read against. None has a counterpart in the reference; bench.py's
 // --floors mode and the profile summaries that quote these floors run them.
+// They are built into libllmik_diag.so (include/llmik_diag.h), apart from
+// the product library, and keep their own last-error text.
 //
 // diag_empty_kernel: a launch that does nothing, the per-dispatch cost of a
 // kernel of the same workgroup size.
@@ -14,13 +16,30 @@
 //
 // diag_read_write_kernel<L, W>: the same read with a write stream of W bytes
 // per 16 bytes read beside it (the KV writers' shape).
+#include <cstdio>
 #include <type_traits>
 
-#include "device_common.hpp"
-#include "llmik_internal.hpp"
+#include "../../include/llmik_diag.h"
+#include "../csrc/device_common.hpp"
 
 namespace llmik {
 namespace {
+
+thread_local char g_diag_error[256] = "";
+
+int set_error(int code, const char* msg) {
+    std::snprintf(g_diag_error, sizeof(g_diag_error), "%s", msg);
+    return code;
+}
+
+int check_launch() {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        std::snprintf(g_diag_error, sizeof(g_diag_error), "HIP launch failed: %s", hipGetErrorString(e));
+        return static_cast<int>(e);
+    }
+    return LLMIK_OK;
+}
 
 constexpr int kDiagWaves = 8;
 constexpr size_t kDiagMaxBytes = (size_t)3 << 30;   // offsets stay 32-bit
@@ -92,6 +111,8 @@ __global__ __launch_bounds__(kDiagWaves * kWave) void diag_read_write_kernel(con
 }  // namespace llmik
 
 extern "C" {
+
+LLMIK_API const char* llmik_diag_last_error(void) { return llmik::g_diag_error; }
 
 LLMIK_API llmik_status llmik_diag_empty(int n_workgroups, void* stream) {
     if (n_workgroups <= 0) return llmik::set_error(LLMIK_ERR_INVALID, "llmik_diag_empty: n_workgroups must be > 0");

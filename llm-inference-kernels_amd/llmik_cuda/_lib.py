@@ -67,9 +67,6 @@ _SIGNATURES = {
     "llmik_rope": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "llmik_rope_qkv_append_f16": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "llmik_add_rmsnorm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _p]),
-    "llmik_diag_empty": (_i, [_i, _p]),
-    "llmik_diag_read": (_i, [_p, _sz, _p, _i, _i, _p]),
-    "llmik_diag_read_write": (_i, [_p, _sz, _p, _i, _i, _i, _p]),
     "llmik_silu_mul_halves": (_i, [_p, _p, _l, _i, _p]),
 }
 
@@ -89,3 +86,38 @@ def check(status: int) -> None:
     if status != 0:
         msg = lib.llmik_last_error().decode(errors="replace")
         raise RuntimeError(f"llmik: {msg} (status {status})")
+
+
+# The measurement floors (include/llmik_diag.h) live in a library of their
+# own; only bench.py --floors and their tests load it.
+DIAG_LIB_PATH = LIB_PATH.parent / "libllmik_diag.so"
+_DIAG_SIGNATURES = {
+    "llmik_diag_last_error": (ctypes.c_char_p, []),
+    "llmik_diag_empty": (_i, [_i, _p]),
+    "llmik_diag_read": (_i, [_p, _sz, _p, _i, _i, _p]),
+    "llmik_diag_read_write": (_i, [_p, _sz, _p, _i, _i, _i, _p]),
+}
+_diag = None
+
+
+def diag_lib():
+    """libllmik_diag.so with its signatures set (loaded on first use)."""
+    global _diag
+    if _diag is None:
+        if not DIAG_LIB_PATH.exists():
+            raise ImportError(f"llmik_cuda: {DIAG_LIB_PATH} is missing; build it with "
+                              "`python llm-inference-kernels_amd/build_lib.py`")
+        d = ctypes.CDLL(str(DIAG_LIB_PATH))
+        for name, (res, args) in _DIAG_SIGNATURES.items():
+            fn = getattr(d, name)
+            fn.restype = res
+            fn.argtypes = args
+        _diag = d
+    return _diag
+
+
+def diag_check(status: int) -> None:
+    """check() for the entry points of libllmik_diag.so."""
+    if status != 0:
+        msg = diag_lib().llmik_diag_last_error().decode(errors="replace")
+        raise RuntimeError(f"llmik_diag: {msg} (status {status})")

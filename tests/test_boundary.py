@@ -1,7 +1,8 @@
 """The C ABI boundary and the llmik_cuda host layer, on the CPU.
 
 * libllmik_hip.so loads and exports every entry point include/llmik.h
-  declares, with the ABI version the host layer expects;
+  declares, with the ABI version the host layer expects; the measurement
+  floors of include/llmik_diag.h live in libllmik_diag.so alone;
 * the C layer rejects bad arguments with LLMIK_ERR_* codes and messages
   before touching the GPU (null / misaligned pointers, head_dim != 128,
   seqlen > kv_buf_len, K / group_size rules);
@@ -23,10 +24,11 @@ import torch
 from tests.helpers import ROOT
 
 HEADER = ROOT / "include" / "llmik.h"
+DIAG_HEADER = ROOT / "include" / "llmik_diag.h"
 
 
-def declared_symbols():
-    text = HEADER.read_text()
+def declared_symbols(header=HEADER):
+    text = header.read_text()
     return sorted(set(re.findall(r"LLMIK_API\s+[\w\s\*]+?\b(llmik_\w+)\s*\(", text)))
 
 
@@ -59,11 +61,29 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_library_was_built_for_gfx950_only():
-    from llmik_cuda._lib import LIB_PATH
-    data = LIB_PATH.read_bytes()
-    assert b"gfx950" in data
-    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
-        assert other not in data
+    from llmik_cuda._lib import DIAG_LIB_PATH, LIB_PATH
+    for path in (LIB_PATH, DIAG_LIB_PATH):
+        data = path.read_bytes()
+        assert b"gfx950" in data
+        for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+            assert other not in data
+
+
+def test_measurement_floors_live_in_their_own_library(lib):
+    from llmik_cuda._lib import diag_lib
+    diag = diag_lib()
+    names = declared_symbols(DIAG_HEADER)
+    assert {"llmik_diag_empty", "llmik_diag_read", "llmik_diag_read_write", "llmik_diag_last_error"} <= set(names)
+    for name in names:
+        assert hasattr(diag, name), name
+        assert not hasattr(lib, name), f"{name} is exported by the product library"
+    # argument checks come before any HIP call
+    assert diag.llmik_diag_read(None, 100, None, 1, 4, None) != 0
+    assert "multiple of 16" in diag.llmik_diag_last_error().decode()
+    assert diag.llmik_diag_read_write(16, 64, 16, 5, 1, 4, None) != 0
+    assert "write_bytes_per_16" in diag.llmik_diag_last_error().decode()
+    assert diag.llmik_diag_empty(0, None) != 0
+    assert "n_workgroups" in diag.llmik_diag_last_error().decode()
 
 
 def _err(lib):

@@ -1,4 +1,4 @@
-"""GPU checks of the measurement kernels (csrc/diag.hip) that bench.py
+"""GPU checks of the measurement kernels (libllmik_diag.so, csrc_diag/diag.hip) that bench.py
 --floors times: the plain read must read every byte once (the xor of the
 per-wave values equals the xor of every 32-bit word, computed on the CPU),
 at sizes that end inside a 4 KiB unit and at grids with more waves than
@@ -15,8 +15,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _lib():
-    from llmik_cuda._lib import check, lib
-    return lib, check
+    from llmik_cuda._lib import diag_check, diag_lib
+    return diag_lib(), diag_check
 
 
 def _stream():
