@@ -33,9 +33,11 @@ constexpr int kWriterThreads = 256;   // 16 token rows of 16 lanes
 constexpr int kTokensPerRow = 2;      // per-token writer: tokens per 16-lane row
 
 // Per token: one DPP row (16 lanes) per token, lane c owns channels
-// 8c..8c+7. A workgroup covers 16 * kTokensPerRow consecutive tokens; the
-// row's loads for all its tokens are issued before any is used (token
+// 8c..8c+7. A workgroup covers 16 * kTokensPerRow consecutive tokens (token
 // i * 16 + row of the workgroup's block, so each i reads 4 KiB contiguous).
+// The compiler issues token i + 1's load after token i's data has arrived,
+// so that token i's arithmetic overlaps it; forcing every load out first
+// (a scheduling barrier) measured slower (INT8 B=8 S=4096 18.7 -> 19.7 us).
 struct TokenMap {
     uint32_t n_tok;     // tokens per (batch, kv_head) row to quantise
     uint32_t src_len;   // token stride of x
