@@ -795,14 +795,23 @@ struct F16HalfTile {
     static constexpr uint32_t kRow = kHeadDim * 2;
     u32x4 k[4];   // lane (g, c): token c, channels 32 ks + 8 g
     u32x4 v[4];   // lane (g, c): token 4 g + e, channels 8 c
+    // Cache policy (aux bits: 1 = sc0, 2 = nt): K non-temporal, V sc0 and
+    // non-temporal. Against K cacheable and V non-temporal (the 32-token
+    // tile's policy, which stays faster there), on three boxes (us): A16
+    // 24.8-25.2 -> 23.2-24.3 (12 reps on one box all at 24.1-24.3; a second
+    // box half of 8 reps at 23.2-23.5, half at 25.4-26.5), B=16 S=4096
+    // 43.9-44.0 -> 41.4-41.5, B=8 S=8192 49.5-53.9 -> 43.0-45.6, B=8 S=2048
+    // 14.9 -> 14.7, but B=4 S=4096 15.2-15.5 -> 15.4-16.3. K non-temporal
+    // with V non-temporal, or sc0 on both, fell into a ~30 us mode on 7 of
+    // 12 A16 reps on one box; this pair did not.
     __device__ __forceinline__ void load(const TileCtx& x, int t0) {
         const uint32_t so = (uint32_t)t0 * kRow;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-            k[ks] = __builtin_amdgcn_raw_buffer_load_b128(x.rk, (int)x.koff, (int)(so + 64 * ks), 0);
+            k[ks] = __builtin_amdgcn_raw_buffer_load_b128(x.rk, (int)x.koff, (int)(so + 64 * ks), 2);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            v[e] = __builtin_amdgcn_raw_buffer_load_b128(x.rv, (int)x.voff, (int)(so + kRow * e), 2);
+            v[e] = __builtin_amdgcn_raw_buffer_load_b128(x.rv, (int)x.voff, (int)(so + kRow * e), 3);
     }
     // B operand of PV MFMA j (channels 8 c + j): V[4 g + e][8 c + j], e = 0..3.
     __device__ __forceinline__ f16x4 vop(int j) const {
