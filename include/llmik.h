@@ -322,9 +322,10 @@ LLMIK_API void llmik_w4a16_set_plan_override(int stream_mode, int stream_splits)
  * Plan knob of the fp16 attention entry points, for measurement and tests (no
  * reference counterpart). f16_half_tiles: 1 runs every fp16 call on the MFMA
  * path with 16-token tiles, 0 with 32-token tiles, -1 restores the rule (16-
- * token tiles for at least 32 (batch, kv head, head chunk) slabs and 2-8
- * 32-token tiles per wave). Not synchronised with calls in flight on other
- * threads.
+ * token tiles for at least 32 (batch, kv head, head chunk) slabs, a
+ * workgroup count that is a multiple of the CU count, and at least two
+ * 32-token tiles per wave unless the workgroups have 4 waves). Not
+ * synchronised with calls in flight on other threads.
  */
 LLMIK_API void llmik_attention_set_plan_override(int f16_half_tiles);
 

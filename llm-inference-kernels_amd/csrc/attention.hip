@@ -1199,15 +1199,25 @@ AttnPlan plan_attention(int batch, int n_heads, int n_kv_heads, int seqlen) {
     return pl;
 }
 
-// fp16 16-token tiles (decode_attention_f16h_kernel) against 32-token ones,
-// on one box (us, 32 -> 16): B=4 S=4096 16.06 -> 15.33, B=8 S=2048 15.59 ->
-// 15.21, B=8 S=4096 26.26 -> 25.05, B=8 S=8192 46.03 -> 45.48, B=16 S=4096
-// 46.11 -> 43.47, B=4 S=8192 26.50 -> 26.11; slower with one tile per wave
-// (B=4 S=2048 10.54 -> 11.47, B=2 S=4096 11.79 -> 12.21, B=8 S=1024) and
-// with 16 (B=8 S=16384 84.8 -> 87.3); about even at B=1-2 S=8192-16384 with
-// fewer than 32 workgroups per split, B=16 S=2048, B=32-64. The rule: at
-// least 32 (batch, kv head, head chunk) slabs and 2-8 32-token tiles per
-// wave. The override (llmik_attention_set_plan_override) forces either.
+// fp16 16-token tiles (decode_attention_f16h_kernel, with its cache policy)
+// against 32-token ones, forced through the override, two boxes, four
+// interleaved reps each (median us, 32 -> 16): B=8 S=4096 25.69 -> 24.65,
+// B=16 S=4096 45.34 -> 41.79, B=32 S=1024 23.28 -> 21.51, B=16 S=1024 15.04
+// -> 14.08, B=32 S=2048 41.70 -> 39.42, B=32 S=4096 79.92 -> 75.89, B=16
+// S=8192 82.25 -> 78.56, B=8 S=16384 83.17 -> 79.82, B=8 S=2048 15.58 ->
+// 14.89, B=64 S=4096 155.03 -> 150.79, B=64 S=8192 308.86 -> 300.36, B=4
+// S=4096 15.96 -> 15.57, B=4 S=8192 26.61 -> 26.21, B=8 S=1024 10.26-10.37
+// -> 10.06-10.22; slower where the grid does not fill the chip in whole
+// rounds (B=12 S=4096, 288 workgroups, 46.60 -> 50.40; B=24 S=4096, 384,
+// 73.16 -> 73.94; B=48 S=2048, 384, 69.07 -> 70.09), with fewer than 32
+// slabs (B=1 S=4096 9.29 -> 9.75, B=2 S=16384 28.08 -> 29.87) and with one
+// tile per 8-wave wave (B=4 S=2048 10.51 -> 10.85); even at B=8 S=32768
+// (163.78 -> 163.88). The rule: at least 32 (batch, kv head, head chunk)
+// slabs, a workgroup count that is a multiple of the CU count, and at least
+// two 32-token tiles per wave unless the workgroups have 4 waves. It takes
+// the faster form at 24 of these 26 shapes (the earlier rule, 2-8 tiles per
+// wave, at 16). The override (llmik_attention_set_plan_override) forces
+// either.
 namespace {
 std::atomic<int> g_f16_tiles{-1};   // -1: the rule, 0: 32-token tiles, 1: 16-token tiles
 }  // namespace
@@ -1221,7 +1231,8 @@ static bool use_f16_half_tiles(const AttnPlan& pl, int seqlen) {
     if (mode >= 0) return mode == 1;
     const long tiles = (seqlen + kTile - 1) / kTile;
     const long per_wave = (tiles + (long)pl.n_splits * pl.waves - 1) / ((long)pl.n_splits * pl.waves);
-    return pl.n_slot_groups >= 32 && per_wave >= 2 && per_wave <= 8;
+    const long wgs = (long)pl.n_slot_groups * pl.n_splits;
+    return pl.n_slot_groups >= 32 && wgs % device_cu_count() == 0 && (per_wave >= 2 || pl.waves == 4);
 }
 
 template <KvFormat F, int HPW>

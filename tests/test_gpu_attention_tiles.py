@@ -3,9 +3,10 @@
 fp16 calls on the MFMA path run either 32-token tiles
 (decode_attention_mfma_kernel) or 16-token tiles with the next tile in
 flight (decode_attention_f16h_kernel); the planner picks the 16-token form
-for at least 32 (batch, kv head, head chunk) slabs and 2-8 32-token tiles per
-wave. Here each case runs under both (llmik_attention_set_plan_override) and
-under the rule:
+for at least 32 (batch, kv head, head chunk) slabs, a workgroup count that is
+a multiple of the CU count, and at least two 32-token tiles per wave unless
+the workgroups have 4 waves. Here each case runs under both
+(llmik_attention_set_plan_override) and under the rule:
 * both are within 2e-3 max-abs of the float64 oracle;
 * the rule's call equals the forced call of the form the rule names, bit for
   bit (the knob and the rule reach the same kernel);
@@ -51,11 +52,11 @@ CASES = [
     (16, 32, 8, 2053, 2053, True),    # a 5-token last tile, 2 splits
     (4, 32, 8, 8191, 8192, True),     # live length 8191 of 8192: a 15-token last tile
     (8, 16, 8, 3000, 3500, True),     # two heads per workgroup, poisoned tail past 3000
-    (32, 8, 8, 1500, 1500, False),    # MHA, 256 slabs, no split: 12 tiles per wave
+    (32, 8, 8, 1500, 1500, True),     # MHA, 256 slabs, no split: 4 waves, 12 tiles per wave
     (2, 32, 8, 4096, 4096, False),    # 16 slabs
-    (8, 32, 8, 1024, 1024, False),    # 4-wave workgroups, 1 tile per wave
+    (8, 32, 8, 1024, 1024, True),     # 4-wave workgroups (512), 1 tile per wave
     (4, 64, 8, 2000, 2000, True),     # GQA 8: two head chunks per kv head
-    (8, 24, 8, 2000, 2000, True),     # GQA 3: one head per workgroup, three chunks per kv head
+    (8, 24, 8, 2000, 2000, False),    # GQA 3: one head per workgroup, three chunks per kv head (384 workgroups)
 ]
 
 
