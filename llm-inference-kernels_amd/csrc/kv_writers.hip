@@ -29,15 +29,11 @@
 
 namespace llmik {
 
-constexpr int kWriterThreads = 256;   // 16 token rows of 16 lanes
-constexpr int kTokensPerRow = 2;      // per-token writer: tokens per 16-lane row
+constexpr int kWriterThreads = 256;   // 32 token groups of 8 lanes, or 16 rows of 16 lanes
 
-// Per token: one DPP row (16 lanes) per token, lane c owns channels
-// 8c..8c+7. A workgroup covers 16 * kTokensPerRow consecutive tokens (token
-// i * 16 + row of the workgroup's block, so each i reads 4 KiB contiguous).
-// The compiler issues token i + 1's load after token i's data has arrived,
-// so that token i's arithmetic overlaps it; forcing every load out first
-// (a scheduling barrier) measured slower (INT8 B=8 S=4096 18.7 -> 19.7 us).
+// Token indexing of the writers: `flat` runs over the n_tok tokens of every
+// (batch, kv_head) row; src / dst give the token's position in x and in the
+// destination cache.
 struct TokenMap {
     uint32_t n_tok;     // tokens per (batch, kv_head) row to quantise
     uint32_t src_len;   // token stride of x
@@ -53,53 +49,88 @@ struct TokenMap {
     }
 };
 
-// MAPPED: tokens go through `map`; otherwise the identity (out-of-place ops,
-// no per-token division).
+// Per token: 8 lanes per token; lane c of an 8-lane group owns channels
+// 8c..8c+7 and 64+8c..64+8c+7, so each load instruction reads the first or
+// the second half of its tokens' rows, contiguous. The per-token work (the
+// 8-lane DPP max, the scale's division, the reciprocal, the addresses) is
+// shared by 16 values per lane. The absmax runs on the fp16 bit patterns
+// (sign masked, packed unsigned max), the same order as the fp32 magnitudes
+// (NaN above +inf). A workgroup covers 32 groups x kTokensPerRow8
+// consecutive tokens. Against 16 lanes per token with 8 values each (two
+// tokens per lane group), same bits, on one box (us): INT8 B=8 S=4096 18.87
+// -> 18.50, INT4 V 17.79 -> 16.25, INT8 / INT4 V B=64 131.8 / 120.7 ->
+// 125.5 / 110.2, S=1000 6.62 / 6.48 -> 6.27 / 5.95; two tokens per group
+// (64 per workgroup) was slower for INT8 (20.4) and at small shapes.
+constexpr int kTokensPerRow8 = 1;
+
+__device__ __forceinline__ uint32_t row8_umax(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppQuadXor1, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppQuadXor2, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kDppRowHalfMirror, 0xF, 0xF, true));
+    return v;
+}
+
 template <int QMAX, bool PACK4, bool MAPPED>
 __global__ __launch_bounds__(kWriterThreads) void quantize_per_token_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, uint16_t* __restrict__ scale,
     long rows, TokenMap map) {
-    const long blk = (long)blockIdx.x * (16 * kTokensPerRow);
-    const int rr = threadIdx.x >> 4;
-    const int c = threadIdx.x & 15;
-    u32x4 raw[kTokensPerRow];
+    constexpr int kGroups = kWriterThreads / 8;
+    const long blk = (long)blockIdx.x * (kGroups * kTokensPerRow8);
+    const int grp = threadIdx.x >> 3;
+    const int c = threadIdx.x & 7;
+    u32x4 raw[kTokensPerRow8][2];
 #pragma unroll
-    for (int i = 0; i < kTokensPerRow; ++i) {
-        // Tokens past the end still take part in the DPP reduction (on a
-        // clamped, in-bounds token) but store nothing.
-        const long flat = min(blk + 16 * i + rr, rows - 1);
+    for (int i = 0; i < kTokensPerRow8; ++i) {
+        // Tokens past the end take part in the DPP reduction on a clamped,
+        // in-bounds token but store nothing.
+        const long flat = min(blk + kGroups * i + grp, rows - 1);
         const long src = MAPPED ? map.src((uint32_t)flat) : flat;
-        raw[i] = stream16(x + src * 128 + 8 * c);
+        raw[i][0] = stream16(x + src * 128 + 8 * c);
+        raw[i][1] = stream16(x + src * 128 + 64 + 8 * c);
     }
 #pragma unroll
-    for (int i = 0; i < kTokensPerRow; ++i) {
-        const long flat = blk + 16 * i + rr;
-        float xf[8];
-        f16x8_to_f32(raw[i], xf);
-        uint32_t amax = 0u;   // NaN-propagating absmax, as bits
+    for (int i = 0; i < kTokensPerRow8; ++i) {
+        const long flat = blk + kGroups * i + grp;
+        // |x| of the 16 fp16 values as bit patterns, packed max per half.
+        uint32_t m = 0u;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) amax = max(amax, abs_bits(xf[e]));
-        amax = row16_umax(amax);
-
-        const float sc = sym_scale(amax, (float)QMAX);
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t a = raw[i][h][d] & 0x7FFF7FFFu;
+                m = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(
+                        __builtin_bit_cast(u16x2, m), __builtin_bit_cast(u16x2, a)));
+            }
+        const uint32_t m16 = max(m & 0xFFFFu, m >> 16);
+        const uint32_t amax16 = row8_umax(m16);
+        const float amax = h2f((uint16_t)amax16);   // exact; NaN stays NaN, inf stays inf
+        const float sc = sym_scale(__float_as_uint(amax), (float)QMAX);
         const float rcp = recip_approx(sc);
-        int code[8];
+        float xf[16];
+        f16x8_to_f32(raw[i][0], xf);
+        f16x8_to_f32(raw[i][1], xf + 8);
+        int code[16];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) code[e] = sym_code(xf[e], sc, rcp, QMAX);
+        for (int e = 0; e < 16; ++e) code[e] = sym_code(xf[e], sc, rcp, QMAX);
         if (flat < rows) {
             const long row = MAPPED ? map.dst((uint32_t)flat) : flat;
             if constexpr (PACK4) {
-                uint32_t w = 0;
+                uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) w |= (uint32_t)(code[e] & 0xF) << (4 * e);
-                __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(q + row * 64 + 4 * c));
+                for (int e = 0; e < 8; ++e) {
+                    w0 |= (uint32_t)(code[e] & 0xF) << (4 * e);
+                    w1 |= (uint32_t)(code[8 + e] & 0xF) << (4 * e);
+                }
+                __builtin_nontemporal_store(w0, reinterpret_cast<uint32_t*>(q + row * 64 + 4 * c));
+                __builtin_nontemporal_store(w1, reinterpret_cast<uint32_t*>(q + row * 64 + 32 + 4 * c));
             } else {
-                u32x2 w;
-                w[0] = (uint32_t)(code[0] & 0xFF) | ((uint32_t)(code[1] & 0xFF) << 8) |
-                       ((uint32_t)(code[2] & 0xFF) << 16) | ((uint32_t)(code[3] & 0xFF) << 24);
-                w[1] = (uint32_t)(code[4] & 0xFF) | ((uint32_t)(code[5] & 0xFF) << 8) |
-                       ((uint32_t)(code[6] & 0xFF) << 16) | ((uint32_t)(code[7] & 0xFF) << 24);
-                __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(q + row * 128 + 8 * c));
+                uint32_t w[4];
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+                    w[d] = (uint32_t)(code[4 * d] & 0xFF) | ((uint32_t)(code[4 * d + 1] & 0xFF) << 8) |
+                           ((uint32_t)(code[4 * d + 2] & 0xFF) << 16) | ((uint32_t)(code[4 * d + 3] & 0xFF) << 24);
+                __builtin_nontemporal_store(u32x2{w[0], w[1]}, reinterpret_cast<u32x2*>(q + row * 128 + 8 * c));
+                __builtin_nontemporal_store(u32x2{w[2], w[3]}, reinterpret_cast<u32x2*>(q + row * 128 + 64 + 8 * c));
             }
             if (c == 0) scale[row] = f2h_bits(sc);
         }
@@ -240,7 +271,7 @@ int launch_quantize_per_token(const void* x, void* q, void* scale, int rows, int
     const long total = (long)rows * n_tok;
     if (total == 0) return LLMIK_OK;
     if (total > 0x7FFFFFFFL) return set_error(LLMIK_ERR_UNSUPPORTED, "too many tokens");
-    const long rows_per_wg = 16 * kTokensPerRow;
+    const long rows_per_wg = (kWriterThreads / 8) * kTokensPerRow8;
     const long grid = (total + rows_per_wg - 1) / rows_per_wg;
     const TokenMap map{(uint32_t)n_tok, (uint32_t)src_len, (uint32_t)dst_len, (uint32_t)dst_off};
     auto xp = static_cast<const uint16_t*>(x);
