@@ -217,12 +217,14 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c1, float s1
 // correctly rounded quotient (256 * (2^-23 + 2^-24 + 2^-24)), so both round
 // to the same integer unless y lies that close to a half-integer; within
 // 2^-12 of one (a tie of the true quotient rounds to even, a near-tie may go
-// either way) the true division runs. NaN and infinite quotients come out
+// either way) the true division runs. As |y - k| <= 0.5 for k = rint(y),
+// "within 2^-12 of a half-integer" is |y - k| >= 0.5 - 2^-12 (one compare,
+// no second subtraction). NaN and infinite quotients (y - k is NaN) come out
 // of the fast path unchanged.
 __device__ __forceinline__ float quant_round(float x, float s, float r) {
     const float y = x * r;
     const float k = __builtin_rintf(y);
-    if (fabsf(fabsf(y - k) - 0.5f) <= 0x1p-12f) return __builtin_rintf(x / s);
+    if (fabsf(y - k) >= 0.5f - 0x1p-12f) return __builtin_rintf(x / s);
     return k;
 }
 

@@ -14,7 +14,7 @@ F = np.float32
 def _rule(x, s, r, fallback=True):
     y = (x * r).astype(F)
     k = np.rint(y)
-    near = np.abs(np.abs((y - k).astype(F)) - F(0.5)) <= F(2.0 ** -12)
+    near = np.abs((y - k).astype(F)) >= F(0.5) - F(2.0 ** -12)
     if not fallback:
         return k
     return np.where(near, np.rint((x / s).astype(F)), k)
@@ -46,3 +46,32 @@ def test_planted_no_fallback_fails():
     x, s = _cases(rng, qmax=127)
     r = np.nextafter((F(1.0) / s).astype(F), F(np.inf)).astype(F)
     assert not np.array_equal(_rule(x, s, r, fallback=False), np.rint((x / s).astype(F)))
+
+
+def test_near_tie_window_forms_agree():
+    """|y - k| >= 0.5 - 2^-12 (the kernels' form) selects the same y as
+    ||y - k| - 0.5| <= 2^-12 for k = rint(y), |y - k| <= 0.5: on fp32 values
+    around half-integers (every ulp step within 2^-11 of them, |y| up to
+    300), random ones, exact ties and integers."""
+    rng = np.random.default_rng(3)
+    centers = np.arange(-300, 300, dtype=F) + F(0.5)
+    ys = [centers, np.arange(-300, 300, dtype=F)]
+    for c in (centers[::7], centers[3::11]):
+        y = c.copy()
+        for _ in range(600):                      # walk ulp by ulp out of the window
+            y = np.nextafter(y, F(np.inf)).astype(F)
+            ys.append(y.copy())
+        y = c.copy()
+        for _ in range(600):
+            y = np.nextafter(y, F(-np.inf)).astype(F)
+            ys.append(y.copy())
+    ys.append(rng.uniform(-300, 300, 200_000).astype(F))
+    y = np.concatenate(ys).astype(F)
+    k = np.rint(y)
+    d = np.abs((y - k).astype(F))
+    assert (d <= F(0.5)).all()
+    old = np.abs((d - F(0.5)).astype(F)) <= F(2.0 ** -12)
+    new = d >= F(0.5) - F(2.0 ** -12)
+    assert np.array_equal(old, new)
+    assert new.any() and (~new).any()
+
