@@ -84,6 +84,7 @@ struct GemmPlan {
                        // 4: MFMA GEMV over up to 16 rows,
                        // 5: streaming MFMA GEMV, 1 <= M <= 16, N % 64 == 0
                        // 6: 32x32x16 MFMA GEMM, M > 16, N % 128 == 0
+                       // 7: 32x32x16 MFMA GEMM, both operands in LDS, M >= 256, N % 128 == 0, K % 64 == 0
     int cols_per_lane; // 4 (16-byte weight loads) or 1
     int tile_n;        // output columns per workgroup
     int tile_m;        // output rows per workgroup

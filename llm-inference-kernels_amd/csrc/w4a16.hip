@@ -1644,6 +1644,340 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
 }
 
 // ---------------------------------------------------------------------------
+// M >= 256 on 32x32x16 matrix cores (plan kind 7; N % 128 == 0, K % 64 == 0,
+// group size a power of two >= 32).
+//
+// A workgroup of 8 waves computes a tile of 256 rows by 128 columns over one
+// K split, in stages of 64 K, with both operands in LDS as fp16 rows of 128
+// bytes (64 K values). The 16-byte chunk j of row r sits in slot j ^ (r % 8)
+// of the row, so the fragment reads of 8 consecutive rows (same chunk) and
+// the chunk stores of 8 consecutive rows hit distinct banks.
+//   * Activations go from memory straight into LDS (buffer_load ... lds, 1
+//     KiB of 8 swizzled rows per instruction, four per wave per stage; rows
+//     past M read zeros) into a three-slot ring, two stages ahead.
+//   * Weight words (the stage's 8 packed rows x 128 columns, two per thread)
+//     and group scales are loaded into registers two stages ahead. Halfway
+//     through a stage's MFMAs the words of the next stage are dequantised
+//     once for the whole workgroup into the exact fp16 codes of their 8 K
+//     positions in K order (i4x8_to_f16_natural) and stored as their
+//     columns' chunks of the next stage's slot (two slots).
+// Wave w computes rows 64 (w % 4) .. + 63 and columns 64 (w / 4) .. + 63 as
+// 2 x 2 blocks of v_mfma_f32_32x32x16_f16; an A or B fragment is one 16-byte
+// LDS read (lane (h, c): row / column 32 blk + c, chunk 2 kc + h of the
+// stage), read one chunk ahead of its MFMAs. Products accumulate per scale
+// group in fp32 from a zero C operand and are scaled at the group's end,
+// acc += scale[g][n] * C_g, so no weight is rounded. One barrier per stage.
+// Against the 64 x 128 tiles of kind 6 each weight word is dequantised once
+// per 256 rows instead of once per 64, and the activations are neither
+// permuted nor staged through registers.
+// ---------------------------------------------------------------------------
+constexpr int kL7TN = 128;
+constexpr int kL7TM = 256;
+constexpr int kL7Waves = 8;
+constexpr int kL7Threads = kL7Waves * kWave;
+
+// Eight int4 codes of one word -> four fp16 pairs in K order, exact: pair i
+// holds the codes of K positions (2i, 2i + 1). Byte i of the word (code 2i
+// in bits 0-3, code 2i + 1 in bits 4-7) is copied to bytes 0 and 2; the mask
+// m = 0x00F0000F keeps code 2i in bits 0-3 of the low half and code 2i + 1
+// in bits 4-7 of the high half; x = 0x54806408 turns u = code + 8 (xor 8 per
+// nibble) into 0x6400 | u = 1024 + u and 0x5400 | (u << 4) = 64 + u (the
+// fp16 ulp at 64 is 1/16), and subtracting (1032, 72) leaves the codes.
+// With m and x in VGPRs each pair is one v_perm, one v_bitop3 and one
+// v_pk_add_f16.
+__device__ __forceinline__ u32x4 i4x8_to_f16_natural(uint32_t w, uint32_t m, uint32_t x) {
+    const f16x2 bias = {(f16)1032.0f, (f16)72.0f};
+    u32x4 out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t b = perm_b32(0u, w, 0x0C000C00u | ((uint32_t)i << 16) | (uint32_t)i);
+        out[i] = __builtin_bit_cast(uint32_t, as_f16x2((b & m) ^ x) - bias);
+    }
+    return out;
+}
+
+struct L7Words {
+    uint32_t w[2];      // packed rows (t >> 7) + 4 j of column t & 127
+    uint16_t s[2][2];   // [cb][u]: scales of the groups of chunks 1 and 3
+};
+
+// G32: group size 32 (two group ends per stage, four scale loads per lane
+// per stage; otherwise one group end and two).
+template <bool G32>
+__global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p) {
+    constexpr int kLoads = 4 + 2 + (G32 ? 4 : 2);   // vector memory instructions per stage
+    // Three separate activation slots: the copies into one slot and the
+    // fragment reads of another are then known not to alias, so the reads
+    // do not wait for copies still in flight.
+    __shared__ __attribute__((aligned(16))) uint8_t s_a0[kL7TM * 128];   // 3 x 32 KiB
+    __shared__ __attribute__((aligned(16))) uint8_t s_a1[kL7TM * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t s_a2[kL7TM * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t s_b[2][kL7TN * 128];   // 32 KiB
+    __shared__ uint32_t s_last;
+
+    // (m-tile, split, tile) from the XCD-contiguous order of kind 6.
+    int bid = blockIdx.x;
+    const int nwg = gridDim.x;
+    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+    const int mtile = bid % p.m_tiles_;
+    const int rest = bid / p.m_tiles_;
+    const int split = rest % p.splits;
+    const int tile = rest / p.splits;
+    const int counter = tile * p.m_tiles_ + mtile;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave & 3;
+    const int wn = wave >> 2;
+    const int c = lane & 31;
+    const int h = lane >> 5;
+
+    const int stages = p.K / 64;
+    const int st0 = split * p.wave_steps;   // wave_steps: stages per split
+    const int st1 = min(st0 + p.wave_steps, stages);
+    const int m0 = mtile * kL7TM;
+    const int n0 = tile * kL7TN;
+    const int lcpg = p.gshift + 1;           // log2(16-K chunks per group)
+    const int cpg_mask = (1 << lcpg) - 1;
+
+    const __amdgpu_buffer_rsrc_t rw = make_buffer_rsrc(p.w, (uint32_t)(p.K / 8) * p.N * 4u);
+    const __amdgpu_buffer_rsrc_t ra = make_buffer_rsrc(p.act, (uint32_t)p.M * p.K * 2u);
+    const __amdgpu_buffer_rsrc_t rs = make_buffer_rsrc(p.scale, (uint32_t)(p.K / p.group_size) * p.N * 2u);
+    // Activation copy: instruction i of wave w fills rows 8 (w + 8 i) .. + 7;
+    // lane l writes slot l % 8 of row 8 (w + 8 i) + l / 8, i.e. chunk
+    // (l % 8) ^ (l / 8) of that row. Rows past M point beyond the bound.
+    uint32_t a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + 8 * (wave + 8 * i) + (lane >> 3);
+        a_off[i] = (row < p.M) ? ((uint32_t)row * p.K * 2u + 16u * (uint32_t)((lane & 7) ^ (lane >> 3)))
+                               : 0x80000000u;
+    }
+    const int bn = t & 127;
+    const int bk = t >> 7;
+    const uint32_t w_off = ((uint32_t)bk * p.N + n0 + bn) * 4u;
+    const uint32_t w_four = (uint32_t)p.N * 16u;   // 4 packed rows
+    const uint32_t w_stage = (uint32_t)p.N * 32u;  // 8 packed rows
+    const uint32_t s_off = (uint32_t)(n0 + 64 * wn + c) * 2u;
+    const uint32_t grp_bytes = (uint32_t)p.N * 2u;
+    const uint32_t km = vgpr_const(0x00F0000Fu);
+    const uint32_t kx = vgpr_const(0x54806408u);
+
+    // Loads for stage st (clamped into the split: a stage past it re-reads
+    // the last one, in bounds, and is never used), always issued in full so
+    // that every stage issues the same number of vector memory instructions.
+    auto load_a = [&](uint8_t* slot, int st) {
+        const uint32_t sc = (uint32_t)min(st, st1 - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void*)(slot + 1024 * (wave + 8 * i)), 16,
+                (int)a_off[i], (int)(sc * 128u), 0, 0);
+    };
+    auto load_w = [&](L7Words& g, int st) {
+        const int sc = min(st, st1 - 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            g.w[j] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)(w_off + j * w_four), (int)(sc * w_stage), 0);
+#pragma unroll
+        for (int u = G32 ? 0 : 1; u < 2; ++u) {
+            const uint32_t grp = (uint32_t)((4 * sc + 1 + 2 * u) >> lcpg);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+                g.s[cb][u] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(s_off + 64u * cb),
+                                                                  (int)(grp * grp_bytes), 0);
+        }
+    };
+    auto store_w = [&](const L7Words& g, int st) {
+        uint8_t* slot = &s_b[(st - st0) & 1][0];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            *reinterpret_cast<u32x4*>(slot + bn * 128 + 16 * ((bk + 4 * j) ^ (bn & 7))) =
+                i4x8_to_f16_natural(g.w[j], km, kx);
+    };
+
+    f32x16 acc[2][2], cg[2][2];
+    const f32x16 zero16 = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f,
+                           0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            acc[rb][cb] = zero16;
+            cg[rb][cb] = zero16;
+        }
+    const int ra_row0 = 64 * wm + c;   // + 32 rb; rows and columns are = c (mod 8)
+    const int rb_col0 = 64 * wn + c;   // + 32 cb
+    const int sw = c & 7;
+
+    // One stage: chunk kk = 4 st + kc starts a scale group (or the split)
+    // only at even kc and ends one only at odd kc (groups are >= 2 chunks,
+    // splits whole stages); at kc = 1 only when the group is 32.
+    auto compute = [&](const uint8_t* sa, int st, const uint16_t (&scl)[2][2]) {
+        const uint8_t* sb = &s_b[(st - st0) & 1][0];
+        f16x8 aop[2][2], bop[2][2];   // [parity of kc][block]
+        auto read_frags = [&](int kc) {
+            const int slot = 16 * ((2 * kc + h) ^ sw);
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+                aop[kc & 1][rb] = __builtin_bit_cast(
+                    f16x8, *reinterpret_cast<const u32x4*>(sa + (ra_row0 + 32 * rb) * 128 + slot));
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+                bop[kc & 1][cb] = __builtin_bit_cast(
+                    f16x8, *reinterpret_cast<const u32x4*>(sb + (rb_col0 + 32 * cb) * 128 + slot));
+        };
+        read_frags(0);
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+            const int kk = 4 * st + kc;
+            if (kc < 3) read_frags(kc + 1);
+            const int x = kc & 1;
+            if ((kc & 1) == 0 && (((kk & cpg_mask) == 0) || kk == 4 * st0)) {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb)
+                        cg[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[x][rb], bop[x][cb], zero16, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb)
+                        cg[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[x][rb], bop[x][cb], cg[rb][cb], 0, 0, 0);
+            }
+            if ((kc == 3 || (G32 && kc == 1)) && (((kk & cpg_mask) == cpg_mask) || kk == 4 * st1 - 1)) {
+                const float s0 = h2f(scl[0][kc >> 1]);
+                const float s1 = h2f(scl[1][kc >> 1]);
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        acc[rb][0][r] = fmaf(s0, cg[rb][0][r], acc[rb][0][r]);
+                        acc[rb][1][r] = fmaf(s1, cg[rb][1][r], acc[rb][1][r]);
+                    }
+            }
+        }
+    };
+
+    // Prologue: stages st0 and st0 + 1 in flight, st0's weights dequantised.
+    // In the loop, stage st issues stage st + 2's loads, dequantises stage
+    // st + 1's words halfway through its MFMAs, and before its barrier waits
+    // for every load but the ones it issued itself (stage st + 1's
+    // activations are then in LDS).
+    L7Words wcur, wnext, wfar;   // stages st, st + 1, st + 2
+    load_a(s_a0, st0);
+    load_w(wcur, st0);
+    load_a(s_a1, st0 + 1);
+    load_w(wnext, st0 + 1);
+    store_w(wcur, st0);
+    __builtin_amdgcn_s_waitcnt(kLoads | 0x0F70);   // vmcnt(kLoads): stage st0's loads are complete
+    __syncthreads();
+    // Stage st reads activation slot (st - st0) % 3 and fills slot
+    // (st - st0 + 2) % 3; the loop is unrolled by three so that every slot
+    // is a fixed array.
+    auto stage = [&](uint8_t* cur, uint8_t* far, int st) {
+        load_a(far, st + 2);
+        load_w(wfar, st + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        const bool more = st + 1 < st1;   // workgroup-uniform
+        compute(cur, st, wcur.s);
+        if (more) store_w(wnext, st + 1);
+        // Every load but this stage's kLoads (4 copies, 2 words, the scales)
+        // is complete, so stage st + 1's activations are in LDS, and this
+        // wave's weight chunk stores are done; then the workgroup barrier. A
+        // bare s_barrier: __syncthreads' release fence would also wait for
+        // the copies of stage st + 2 issued above. The memory clobber keeps
+        // the compiler from moving LDS accesses across it.
+        __builtin_amdgcn_s_waitcnt(kLoads | (7 << 4));   // vmcnt(kLoads) lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+        wcur = wnext;
+        wnext = wfar;
+    };
+    for (int st = st0; st < st1; st += 3) {
+        stage(s_a0, s_a2, st);
+        if (st + 1 >= st1) break;
+        stage(s_a1, s_a0, st + 1);
+        if (st + 2 >= st1) break;
+        stage(s_a2, s_a1, st + 2);
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the loads past the split land before the LDS is reused
+
+    // C layout of v_mfma_f32_32x32x16: value r of lane l is row 8 (r / 4) +
+    // 4 (l / 32) + r % 4, column l % 32 of the block. The epilogue uses buffer
+    // accesses bounded by M rows: stores to rows past M are dropped and loads
+    // from them return zeros, so no access needs a row test.
+    const uint32_t esz = p.f32_out ? 4u : 2u;
+    const uint32_t slab = (uint32_t)p.M * p.N;   // elements per split (plan: M N 4 < 2^31)
+    const __amdgpu_buffer_rsrc_t ro = make_buffer_rsrc(p.out, slab * esz);
+    uint32_t eoff[2];                            // element offset of value r = 0 of block row rb
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) eoff[rb] = (uint32_t)(m0 + 64 * wm + 32 * rb + 4 * h) * p.N + n0 + 64 * wn + c;
+    auto roff = [&](int r) { return (uint32_t)(8 * (r >> 2) + (r & 3)) * p.N; };
+    auto store_res = [&](int rb, int cb, int r, float v) {
+        const uint32_t e = eoff[rb] + roff(r) + 32 * cb;
+        if (p.f32_out) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ro, (int)(e * 4u), 0, 0);
+        else __builtin_amdgcn_raw_buffer_store_b16(f2h_bits(v), ro, (int)(e * 2u), 0, 0);
+    };
+    if (p.splits == 1) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) store_res(rb, cb, r, acc[rb][cb][r]);
+        return;
+    }
+    auto part_rsrc = [&](int sp) { return make_buffer_rsrc(p.part + (long)sp * slab, slab * 4u); };
+    {
+        const __amdgpu_buffer_rsrc_t rp = part_rsrc(split);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[rb][cb][r]), rp,
+                                                          (int)((eoff[rb] + roff(r) + 32 * cb) * 4u), 0, kPublishAux);
+    }
+    publish_wait();
+    __syncthreads();
+    if (t == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u) return;
+    // Last split of the tile: the partials are added in split order (this
+    // workgroup's own from registers, the same bits it stored), one block row
+    // at a time, all loads of one split issued together.
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        f32x16 tot[2] = {zero16, zero16};
+        for (int sp = 0; sp < p.splits; ++sp) {
+            if (sp == split) {
+                tot[0] += acc[rb][0];
+                tot[1] += acc[rb][1];
+                continue;
+            }
+            const __amdgpu_buffer_rsrc_t rp = part_rsrc(sp);
+            f32x16 x[2];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    x[cb][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        rp, (int)((eoff[rb] + roff(r) + 32 * cb) * 4u), 0, kPublishAux));
+            tot[0] += x[0];
+            tot[1] += x[1];
+        }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) store_res(rb, cb, r, tot[cb][r]);
+    }
+    if (t == 0) p.counters[counter] = 0u;
+}
+
+// ---------------------------------------------------------------------------
 // M > 1: each lane owns COLS columns and MT rows; the weight is dequantised
 // once per packed word into fp32 (code * scale, exact) and reused across the
 // MT rows. Grid z walks the row tiles.
@@ -1818,6 +2152,10 @@ __global__ __launch_bounds__(256) void w4a16_dequantize_kernel(const uint32_t* _
 // LLMIK_W4A16_STREAM_SPLITS when the library loads, and settable with
 // llmik_w4a16_set_plan_override.
 constexpr long kStreamMinWeightBytes = 8L << 20;
+// Rows from which the 256 x 128 LDS-staged GEMM (kind 7) serves M > 16.
+#ifndef LLMIK_W4A16_LDS_MIN_M
+#define LLMIK_W4A16_LDS_MIN_M 256
+#endif
 
 namespace {
 int env_int(const char* name, bool as_flag) {
@@ -1945,6 +2283,40 @@ static GemmPlan plan_w4a16_mode(int M, int N, int K, int group_size, int stream_
         pl.m_tiles = 1;
         pl.kp_per_split = 4 * sps;
         pl.splits = (steps + sps - 1) / sps;
+        pl.off_part = kCounterBytes;
+        pl.workspace_bytes =
+            (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
+        return pl;
+    }
+    if (M >= LLMIK_W4A16_LDS_MIN_M && N % 128 == 0 && pow2_group && K % 64 == 0 &&
+        (long)(K / 8) * N * 4 < (1L << 31) && (long)M * K * 2 < (1L << 31) &&
+        (long)M * N * 4 < (1L << 31) &&
+        3L * ((M + kL7TM - 1) / kL7TM) * (N / kL7TN) > device_cu_count()) {
+        // 256 x 128 tiles with both operands staged in LDS; K splits (whole
+        // scale groups where they allow) until the tiles fill the CUs once.
+        // Chosen over kind 6 when its tiles need at most 2 splits (its split
+        // hand-off is slower than kind 6's, and with 4 or more splits kind 6
+        // is as fast or faster: M=512 (4096, 4096) 25.6 against 32.5 us,
+        // (14336, 4096) 77.2 against 76.0; M=768, 2 splits, 46.8 -> 44.4 and
+        // 137.5 -> 126.4).
+        const int stages = K / 64;
+        pl.kind = 7;
+        pl.cols_per_lane = 2;
+        pl.tile_n = kL7TN;
+        pl.tile_m = kL7TM;
+        pl.n_tiles = N / kL7TN;
+        pl.m_tiles = (M + kL7TM - 1) / kL7TM;
+        const long base = (long)pl.n_tiles * pl.m_tiles;
+        long want = device_cu_count() / base;
+        if (base > kMaxCounters) want = 1;
+        if (want < 1) want = 1;
+        int sps = (int)((stages + want - 1) / want);
+        const int spg = group_size / 64;   // stages per scale group (0 when it is 32)
+        if (spg > 1 && sps > spg) sps = (sps + spg - 1) / spg * spg;
+        pl.wave_steps = sps;
+        pl.waves = kL7Waves;
+        pl.kp_per_split = 8 * sps;
+        pl.splits = (stages + sps - 1) / sps;
         pl.off_part = kCounterBytes;
         pl.workspace_bytes =
             (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
@@ -2157,6 +2529,11 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
         p.vec_out = (reinterpret_cast<uintptr_t>(out) % 16 == 0) ? 1 : 0;
         const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kG32Threads);
         hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel, grid, blk, 0, stream, p);
+    } else if (pl.kind == 7) {
+        p.m_tiles_ = pl.m_tiles;
+        const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kL7Threads);
+        if (group_size == 32) hipLaunchKernelGGL(w4a16_gemm_lds_kernel<true>, grid, blk, 0, stream, p);
+        else hipLaunchKernelGGL(w4a16_gemm_lds_kernel<false>, grid, blk, 0, stream, p);
     } else if (pl.kind == 3) {
         const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kMmaThreads);
         switch (pl.tile_m) {

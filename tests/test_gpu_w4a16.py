@@ -83,19 +83,28 @@ def test_llama_shapes(llmik, cuda, M, K, N):
                                       (24, 32, 128, 32), (40, 96, 128, 32), (127, 2048, 384, 256),
                                       # 2 <= M <= 16 matrix-core GEMV: 32-column tiles, splits,
                                       # a K range that ends inside a batch
-                                      (3, 4096, 96, 128), (16, 1056, 32, 32), (9, 7168, 64, 512)])
+                                      (3, 4096, 96, 128), (16, 1056, 32, 32), (9, 7168, 64, 512),
+                                      # M >= 256 LDS-staged GEMM (256 x 128 tiles, >= 86 of them
+                                      # on 256 CUs): 2 splits with group 32, one split with group
+                                      # 64, 2 splits of whole 256-groups, ragged M with 2 splits
+                                      # of 6 and 4 stages, a 256-group cut by the split boundary
+                                      (257, 256, 5504, 32), (600, 512, 6144, 64), (300, 1024, 6400, 256),
+                                      (1000, 640, 2816, 128), (260, 256, 5632, 256)])
 def test_odd_shapes(llmik, cuda, M, K, N, gs):
     _check(llmik, cuda, M, K, N, gs, seed=M * 7 + K)
 
 
 @pytest.mark.parametrize("M,K,N,f32", [(128, 4096, 4096, False), (128, 4096, 4096, True),
-                                      (300, 128, 256, False)])
+                                      (300, 128, 256, False), (513, 256, 6144, False),
+                                      (300, 512, 6400, True)])
 def test_unaligned_output_pointer(llmik, cuda, M, K, N, f32):
     """The 32x32 GEMM stores 8 / 16 bytes at a time only when the output is
     16-byte aligned. An output 4 bytes off (the C ABI's minimum alignment for
     out; a caller's offset view) takes the per-value stores: same bits as the
     aligned output, nothing written outside it. (128, 4096, 4096) splits K;
-    (300, 128, 256) does not."""
+    (300, 128, 256) does not. (513, 256, 6144) and (300, 512, 6400) run the
+    LDS-staged GEMM (one store per value, rows past M dropped by the buffer
+    bound), without and with a K split."""
     from llmik_cuda._lib import lib
     q, s, packed = _weights(K, N, 128, 5)
     a = _dev(randn((M, K), 6).astype(np.float16), cuda)
@@ -128,7 +137,8 @@ def test_deterministic(llmik, cuda):
 
 
 @pytest.mark.parametrize("M,K,N", [(128, 4096, 4096), (64, 4096, 4096), (128, 14336, 4096),
-                                   (300, 4096, 1024), (100, 384, 128), (40, 2048, 1152)])
+                                   (300, 4096, 1024), (100, 384, 128), (40, 2048, 1152),
+                                   (300, 1024, 6400)])
 def test_split_gemm_repeatable(llmik, cuda, M, K, N):
     """The M > 16 GEMM with K splits (the last split to arrive adds every
     split's partial in split order, its own from registers): the same bits
@@ -152,3 +162,27 @@ def test_dequantize_bit_exact(llmik, cuda, K, N, gs):
     out = llmik.w4a16_dequantize(_dev(packed, cuda), _dev(s, cuda), gs)
     ref = ow.w4a16_dequantize_fp16(packed, s, gs)
     assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(2048, 4096, 4096, 128), (512, 4096, 14336, 128),
+                                      (768, 14336, 4096, 128), (1024, 2048, 4096, 32),
+                                      (2000, 1024, 11008, 64)])
+def test_prefill_sizes_lds_gemm(llmik, cuda, M, K, N, gs):
+    """Prefill sizes on the LDS-staged GEMM (M >= 256 with at least 86
+    256 x 128 tiles): (768, 14336, 4096) with 2 K splits, the others with
+    none, group 32 and 64, ragged M (2000). Reference: act @ (q * scale) in
+    float64 on the GPU (the numpy oracle's formula, restated in torch for
+    these sizes; the oracle itself covers the smaller shapes above). Gate:
+    fp32 output within 2e-3, fp16 output the RNE rounding of the fp32 one,
+    repeat calls bit-identical."""
+    q, s, packed = _weights(K, N, gs, seed=M + K + N + gs)
+    act = randn((M, K), M + 11).astype(np.float16)
+    a, w, sc = _dev(act, cuda), _dev(packed, cuda), _dev(s, cuda)
+    out32 = llmik.w4a16_gemm_f32out(a, w, sc, gs)
+    out16 = llmik.w4a16_gemm(a, w, sc, gs)
+    wq = _dev(q, cuda).double() * _dev(s, cuda).double().repeat_interleave(gs, dim=0)
+    ref = a.double() @ wq
+    assert float((out32.double() - ref).abs().max()) <= TOL
+    assert torch.equal(out16, out32.half())
+    assert torch.equal(llmik.w4a16_gemm_f32out(a, w, sc, gs), out32)
+
