@@ -92,7 +92,9 @@ struct GemmPlan {
     int splits;        // K splits
     int kp_per_split;  // packed K rows (8 K each) per split
     int waves;         // kinds 5, 6: waves per workgroup
-    int wave_steps;    // kinds 5, 6: 32-K steps per wave
+    int wave_steps;    // kinds 5, 6: 32-K steps per wave; kind 7: 64-K stages per split
+    int full_tiles;    // kind 7: leading tiles computed unsplit
+    int split_tiles;   // kind 7: tiles computed in `splits` K splits
     size_t workspace_bytes;
     size_t off_part;
 };

@@ -41,6 +41,7 @@ struct GemmParams {
     int nw;              // streaming GEMV: waves per workgroup
     int wave_steps;      // streaming GEMV / 32x32 GEMM: 32-K steps per wave
     int m_tiles_;        // 32x32 GEMM: row tiles
+    int full_tiles;      // LDS-staged GEMM: leading tiles computed whole (no K split)
     int vec_out;         // 32x32 GEMM: out is 16-byte aligned (vector stores)
     // Streaming GEMV pair epilogues: each 64-column tile holds 32 column
     // pairs (i, i + 32). kEpiSwiglu: see store_swiglu; kEpiQkvRope: see
@@ -1715,15 +1716,45 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
     __shared__ __attribute__((aligned(16))) uint8_t s_b[2][kL7TN * 128];   // 32 KiB
     __shared__ uint32_t s_last;
 
-    // (m-tile, split, tile) from the XCD-contiguous order of kind 6.
-    int bid = blockIdx.x;
-    const int nwg = gridDim.x;
-    if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
-    const int mtile = bid % p.m_tiles_;
-    const int rest = bid / p.m_tiles_;
-    const int split = rest % p.splits;
-    const int tile = rest / p.splits;
-    const int counter = tile * p.m_tiles_ + mtile;
+    // Tiles are numbered m-tile fastest (tl = tile * m_tiles + mtile). The
+    // first full_tiles workgroups (whole rounds of the CUs) compute tiles
+    // 0 .. full_tiles - 1 over all of K, XCD-contiguously when that count is
+    // a multiple of 8
+    // (the dispatcher deals ids to the 8 XCDs round robin). The rest split
+    // the K range of each remaining tile `splits` ways; they are dispatched
+    // last and fill the final round. With full_tiles = 0 every tile is split
+    // and the order is kind 6's (m-tiles, then splits, of a column tile
+    // neighbours on one XCD). A split tile q (its rank among the split
+    // tiles) owns counter q and partial slots q * splits .. + splits - 1.
+    const int F = p.full_tiles;
+    const int bx = blockIdx.x;
+    int mtile, tile, split, nsplit, q;
+    if (bx < F) {
+        const int b = ((F & 7) == 0) ? (bx & 7) * (F >> 3) + (bx >> 3) : bx;
+        mtile = b % p.m_tiles_;
+        tile = b / p.m_tiles_;
+        split = 0;
+        nsplit = 1;
+        q = 0;
+    } else if (F == 0) {
+        int b = bx;
+        const int nwg = gridDim.x;
+        if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
+        mtile = b % p.m_tiles_;
+        const int rest = b / p.m_tiles_;
+        split = rest % p.splits;
+        tile = rest / p.splits;
+        nsplit = p.splits;
+        q = tile * p.m_tiles_ + mtile;
+    } else {
+        const int b = bx - F;
+        q = b / p.splits;
+        split = b % p.splits;
+        const int tl = F + q;
+        mtile = tl % p.m_tiles_;
+        tile = tl / p.m_tiles_;
+        nsplit = p.splits;
+    }
 
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -1734,8 +1765,8 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
     const int h = lane >> 5;
 
     const int stages = p.K / 64;
-    const int st0 = split * p.wave_steps;   // wave_steps: stages per split
-    const int st1 = min(st0 + p.wave_steps, stages);
+    const int st0 = nsplit == 1 ? 0 : split * p.wave_steps;   // wave_steps: stages per split
+    const int st1 = nsplit == 1 ? stages : min(st0 + p.wave_steps, stages);
     const int m0 = mtile * kL7TM;
     const int n0 = tile * kL7TN;
     const int lcpg = p.gshift + 1;           // log2(16-K chunks per group)
@@ -1909,8 +1940,7 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
     // accesses bounded by M rows: stores to rows past M are dropped and loads
     // from them return zeros, so no access needs a row test.
     const uint32_t esz = p.f32_out ? 4u : 2u;
-    const uint32_t slab = (uint32_t)p.M * p.N;   // elements per split (plan: M N 4 < 2^31)
-    const __amdgpu_buffer_rsrc_t ro = make_buffer_rsrc(p.out, slab * esz);
+    const __amdgpu_buffer_rsrc_t ro = make_buffer_rsrc(p.out, (uint32_t)p.M * p.N * esz);   // plan: M N 4 < 2^31
     uint32_t eoff[2];                            // element offset of value r = 0 of block row rb
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) eoff[rb] = (uint32_t)(m0 + 64 * wm + 32 * rb + 4 * h) * p.N + n0 + 64 * wn + c;
@@ -1920,7 +1950,7 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
         if (p.f32_out) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ro, (int)(e * 4u), 0, 0);
         else __builtin_amdgcn_raw_buffer_store_b16(f2h_bits(v), ro, (int)(e * 2u), 0, 0);
     };
-    if (p.splits == 1) {
+    if (nsplit == 1) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -1929,7 +1959,15 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
                 for (int r = 0; r < 16; ++r) store_res(rb, cb, r, acc[rb][cb][r]);
         return;
     }
-    auto part_rsrc = [&](int sp) { return make_buffer_rsrc(p.part + (long)sp * slab, slab * 4u); };
+    // Split partials: tile-local [256][128] fp32 slots.
+    constexpr uint32_t kTileElems = kL7TM * kL7TN;
+    uint32_t loff[2];   // tile-local element offset of value r = 0 of block row rb
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) loff[rb] = (uint32_t)(64 * wm + 32 * rb + 4 * h) * kL7TN + 64 * wn + c;
+    auto lroff = [&](int r) { return (uint32_t)(8 * (r >> 2) + (r & 3)) * kL7TN; };
+    auto part_rsrc = [&](int sp) {
+        return make_buffer_rsrc(p.part + ((long)q * nsplit + sp) * kTileElems, kTileElems * 4u);
+    };
     {
         const __amdgpu_buffer_rsrc_t rp = part_rsrc(split);
 #pragma unroll
@@ -1939,11 +1977,11 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[rb][cb][r]), rp,
-                                                          (int)((eoff[rb] + roff(r) + 32 * cb) * 4u), 0, kPublishAux);
+                                                          (int)((loff[rb] + lroff(r) + 32 * cb) * 4u), 0, kPublishAux);
     }
     publish_wait();
     __syncthreads();
-    if (t == 0) s_last = arrive_last(&p.counters[counter], (uint32_t)p.splits) ? 1u : 0u;
+    if (t == 0) s_last = arrive_last(&p.counters[q], (uint32_t)nsplit) ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;
     // Last split of the tile: the partials are added in split order (this
@@ -1952,7 +1990,7 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
         f32x16 tot[2] = {zero16, zero16};
-        for (int sp = 0; sp < p.splits; ++sp) {
+        for (int sp = 0; sp < nsplit; ++sp) {
             if (sp == split) {
                 tot[0] += acc[rb][0];
                 tot[1] += acc[rb][1];
@@ -1965,7 +2003,7 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     x[cb][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                        rp, (int)((eoff[rb] + roff(r) + 32 * cb) * 4u), 0, kPublishAux));
+                        rp, (int)((loff[rb] + lroff(r) + 32 * cb) * 4u), 0, kPublishAux));
             tot[0] += x[0];
             tot[1] += x[1];
         }
@@ -1974,7 +2012,7 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
 #pragma unroll
             for (int r = 0; r < 16; ++r) store_res(rb, cb, r, tot[cb][r]);
     }
-    if (t == 0) p.counters[counter] = 0u;
+    if (t == 0) p.counters[q] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -2300,26 +2338,54 @@ static GemmPlan plan_w4a16_mode(int M, int N, int K, int group_size, int stream_
         // (14336, 4096) 77.2 against 76.0; M=768, 2 splits, 46.8 -> 44.4 and
         // 137.5 -> 126.4).
         const int stages = K / 64;
+        const int spg = group_size / 64;   // stages per scale group (0 when it is 32)
         pl.kind = 7;
         pl.cols_per_lane = 2;
         pl.tile_n = kL7TN;
         pl.tile_m = kL7TM;
         pl.n_tiles = N / kL7TN;
         pl.m_tiles = (M + kL7TM - 1) / kL7TM;
-        const long base = (long)pl.n_tiles * pl.m_tiles;
-        long want = device_cu_count() / base;
-        if (base > kMaxCounters) want = 1;
+        pl.waves = kL7Waves;
+        const long cus = device_cu_count();
+        const long tiles = (long)pl.n_tiles * pl.m_tiles;
+        // Tiles in whole rounds of the CUs run unsplit; the rest (or all of
+        // them, when they do not fill one round) may split K s ways (s <= 4).
+        // Cost of the rest in stages: rounds ceil(rest * s / CUs) times
+        // (stages / s + 8), plus 4 per round for the hand-off when s > 1 (a
+        // round's prologue, epilogue and hand-off measure ~8 and ~4 stages);
+        // a split is taken when it saves 15 %. M=768 (4096, 14336), 336
+        // tiles: 256 unsplit and 80 in 3 splits, 135 -> 107 us; M=1024, 192
+        // left, stays unsplit (4 splits measured 139 -> 172 us).
+        long full = 0, want = 1, rest = tiles;
+        if (tiles <= cus) {
+            want = cus / tiles;
+        } else {
+            full = tiles / cus * cus;
+            rest = tiles - full;
+            auto cost = [&](long sp) {
+                const long rounds = (rest * sp + cus - 1) / cus;
+                return (double)rounds * ((double)(stages + sp - 1) / sp + 8.0 + (sp > 1 ? 4.0 : 0.0));
+            };
+            const double one = cost(1);
+            double best = 0.85 * one;
+            for (long sp = 2; sp <= 4 && rest > 0; ++sp)
+                if (cost(sp) < best) { best = cost(sp); want = sp; }
+            if (want == 1) full = 0, rest = tiles;   // no split: one plain launch order
+        }
+        if (rest > kMaxCounters) want = 1, full = 0, rest = tiles;
         if (want < 1) want = 1;
+        if (want > stages) want = stages;
         int sps = (int)((stages + want - 1) / want);
-        const int spg = group_size / 64;   // stages per scale group (0 when it is 32)
         if (spg > 1 && sps > spg) sps = (sps + spg - 1) / spg * spg;
         pl.wave_steps = sps;
-        pl.waves = kL7Waves;
         pl.kp_per_split = 8 * sps;
         pl.splits = (stages + sps - 1) / sps;
+        if (pl.splits == 1) full = 0, rest = tiles;
+        pl.full_tiles = (int)full;
+        pl.split_tiles = (int)rest;
         pl.off_part = kCounterBytes;
-        pl.workspace_bytes =
-            (pl.splits > 1) ? kCounterBytes + align_up((size_t)pl.splits * M * N * sizeof(float), 256) : 0;
+        pl.workspace_bytes = (pl.splits > 1)
+            ? kCounterBytes + align_up((size_t)rest * pl.splits * kL7TM * kL7TN * sizeof(float), 256) : 0;
         return pl;
     }
     if (M > 16 && N % 128 == 0 && pow2_group && K % 32 == 0 && (long)(K / 8) * N * 4 < (1L << 31) &&
@@ -2531,7 +2597,8 @@ int launch_w4a16(const void* act, const void* w, const void* scale, void* out, b
         hipLaunchKernelGGL(w4a16_gemm_mfma32_kernel, grid, blk, 0, stream, p);
     } else if (pl.kind == 7) {
         p.m_tiles_ = pl.m_tiles;
-        const dim3 grid(pl.n_tiles * pl.splits * pl.m_tiles), blk(kL7Threads);
+        p.full_tiles = pl.full_tiles;
+        const dim3 grid(pl.full_tiles + pl.split_tiles * pl.splits), blk(kL7Threads);
         if (group_size == 32) hipLaunchKernelGGL(w4a16_gemm_lds_kernel<true>, grid, blk, 0, stream, p);
         else hipLaunchKernelGGL(w4a16_gemm_lds_kernel<false>, grid, blk, 0, stream, p);
     } else if (pl.kind == 3) {

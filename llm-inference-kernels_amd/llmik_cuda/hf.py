@@ -269,10 +269,15 @@ _TARGET_LINEAR_NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "up_proj", "gate
 
 def dequant_path_threshold(N: int) -> int:
     """Rows from which dequantise + matmul (hipBLASLt) beats w4a16_gemm on
-    MI355X, measured at the Llama-3-8B shapes: ~768 rows for N = 4096 (K =
-    4096 or 14336), ~448 for N = 14336. The reference switches at 256
-    (integration/w4a16_patch.py:89), where w4a16_gemm is 1.5-2.2x faster."""
-    return 768 if N <= 8192 else 448
+    MI355X, measured at the Llama-3-8B shapes: w4a16_gemm is faster up to
+    1024 rows for N = 4096 (K = 4096 or 14336; 47.6 against 51.7 us and
+    130.6 against 151.0 at 1024, 71.3 against 63.1 at 1536) and up to 768
+    for N = 14336 (106.9 against 112.5). The reference switches at 256
+    (integration/w4a16_patch.py:89), where w4a16_gemm is 2.0-2.4x faster.
+    Below the threshold the output is also the exact one (fp32 accumulation
+    of unrounded weights, within 2e-3 of the float64 product; the fp16
+    dequantised weights of the other path are not)."""
+    return 1536 if N <= 8192 else 1024
 
 
 class QuantizedLinear(nn.Module):

@@ -157,8 +157,8 @@ def test_w4a16_patch(hf, cuda):
     ref = _run(ref_model, DynamicCache(), prompt, steps)
     assert float((got - ref).abs().max()) <= LOGIT_TOL
     # the prefill-size path (dequantise + matmul) from the crossover on
-    assert hf.dequant_path_threshold(512) == 768 and hf.dequant_path_threshold(14336) == 448
-    x = torch.randn((800, 512), device=cuda, dtype=torch.float16)
+    assert hf.dequant_path_threshold(512) == 1536 and hf.dequant_path_threshold(14336) == 1024
+    x = torch.randn((1600, 512), device=cuda, dtype=torch.float16)
     q = base.model.layers[0].self_attn.q_proj
     W = llmik.w4a16_dequantize(q.weight_packed, q.scale, 128)
     assert torch.equal(q(x), x @ W)

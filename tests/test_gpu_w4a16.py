@@ -166,11 +166,17 @@ def test_dequantize_bit_exact(llmik, cuda, K, N, gs):
 
 @pytest.mark.parametrize("M,K,N,gs", [(2048, 4096, 4096, 128), (512, 4096, 14336, 128),
                                       (768, 14336, 4096, 128), (1024, 2048, 4096, 32),
-                                      (2000, 1024, 11008, 64)])
+                                      (2000, 1024, 11008, 64), (768, 1024, 14336, 128),
+                                      (2048, 4096, 14336, 128), (3072, 1024, 14336, 32)])
 def test_prefill_sizes_lds_gemm(llmik, cuda, M, K, N, gs):
     """Prefill sizes on the LDS-staged GEMM (M >= 256 with at least 86
-    256 x 128 tiles): (768, 14336, 4096) with 2 K splits, the others with
-    none, group 32 and 64, ragged M (2000). Reference: act @ (q * scale) in
+    256 x 128 tiles), on 256 CUs: (768, 14336, 4096) and (1024, 2048, 4096)
+    with every tile in 2 K splits; (768, 1024, 14336) 256 tiles whole and
+    the 80 left in 3 splits of 6, 6 and 4 stages; (2048, 4096, 14336) 768
+    whole and 128 in 2; (3072, 1024, 14336) 1280 whole and 64 in 4 (group
+    32); (2000, 1024, 11008) 688 tiles, unsplit (splitting the 176 left
+    would cost more); the others unsplit. Group 32 and 64, ragged M (2000).
+    Reference: act @ (q * scale) in
     float64 on the GPU (the numpy oracle's formula, restated in torch for
     these sizes; the oracle itself covers the smaller shapes above). Gate:
     fp32 output within 2e-3, fp16 output the RNE rounding of the fp32 one,
