@@ -1657,11 +1657,11 @@ __global__ __launch_bounds__(kG32Threads) void w4a16_gemm_mfma32_kernel(GemmPara
 //     KiB of 8 swizzled rows per instruction, four per wave per stage; rows
 //     past M read zeros) into a three-slot ring, two stages ahead.
 //   * Weight words (the stage's 8 packed rows x 128 columns, two per thread)
-//     and group scales are loaded into registers two stages ahead. Halfway
-//     through a stage's MFMAs the words of the next stage are dequantised
-//     once for the whole workgroup into the exact fp16 codes of their 8 K
-//     positions in K order (i4x8_to_f16_natural) and stored as their
-//     columns' chunks of the next stage's slot (two slots).
+//     and group scales are loaded into registers two stages ahead. After a
+//     stage's MFMAs the words of the next stage are dequantised once for
+//     the whole workgroup into the exact fp16 codes of their 8 K positions
+//     in K order (i4x8_to_f16_natural) and stored as their columns' chunks
+//     of the next stage's slot (two slots).
 // Wave w computes rows 64 (w % 4) .. + 63 and columns 64 (w / 4) .. + 63 as
 // 2 x 2 blocks of v_mfma_f32_32x32x16_f16; an A or B fragment is one 16-byte
 // LDS read (lane (h, c): row / column 32 blk + c, chunk 2 kc + h of the
@@ -1893,9 +1893,9 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
     };
 
     // Prologue: stages st0 and st0 + 1 in flight, st0's weights dequantised.
-    // In the loop, stage st issues stage st + 2's loads, dequantises stage
-    // st + 1's words halfway through its MFMAs, and before its barrier waits
-    // for every load but the ones it issued itself (stage st + 1's
+    // In the loop, stage st issues stage st + 2's loads, runs its MFMAs,
+    // dequantises and stores stage st + 1's words, and before its barrier
+    // waits for every load but the ones it issued itself (stage st + 1's
     // activations are then in LDS).
     L7Words wcur, wnext, wfar;   // stages st, st + 1, st + 2
     load_a(s_a0, st0);
