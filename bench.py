@@ -792,7 +792,7 @@ def bench_floors(steps: int, warmup: int) -> list:
 # ------------------------------------------------------------- HBM traffic
 
 PMC_WORKLOADS = ("attn:fp16", "attn:int8", "attn:int4", "attn:int4g32", "attn:int4b64",
-                 "w4a16:1", "w4a16:16", "w4a16:128")
+                 "w4a16:1", "w4a16:16", "w4a16:128", "w4a16:256", "w4a16:2048")
 
 
 def pmc_workload(llmik, name: str, steps: int) -> None:

@@ -1676,6 +1676,15 @@ constexpr int kL7TN = 128;
 constexpr int kL7TM = 256;
 constexpr int kL7Waves = 8;
 constexpr int kL7Threads = kL7Waves * kWave;
+// LDS-staged GEMM: m-tiles per group in the order of unsplit tiles (0: all
+// of them, i.e. m-tile fastest). With 2, one XCD's 32 concurrent
+// workgroups cover 2 m-tiles x 16 column tiles instead of 8 x 4 (M = 2048),
+// so each XCD streams a quarter of the activation rows: measured on one box
+// against 0, M=3072 (4096, 14336) 433.9 -> 419.3 us, M=4096 579.6 -> 545.4,
+// M <= 2048 within 1.5 % (1 and 4: 421.9 / 548.3 and 423.4 / 545.9).
+#ifndef LLMIK_L7_GM
+#define LLMIK_L7_GM 2
+#endif
 
 // Eight int4 codes of one word -> four fp16 pairs in K order, exact: pair i
 // holds the codes of K positions (2i, 2i + 1). Byte i of the word (code 2i
@@ -1728,11 +1737,20 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
     // tiles) owns counter q and partial slots q * splits .. + splits - 1.
     const int F = p.full_tiles;
     const int bx = blockIdx.x;
+    // Unsplit tiles in groups of G m-tiles: index b -> (m-tile group, column
+    // tile, m-tile in the group), so that consecutive indices (one XCD's
+    // concurrent workgroups) cover G m-tiles of many column tiles.
+    const int G = (LLMIK_L7_GM > 0 && p.m_tiles_ % LLMIK_L7_GM == 0) ? LLMIK_L7_GM : p.m_tiles_;
+    auto tile_of = [&](int b, int& mt, int& nt) {
+        const int mg = b / (G * p.n_tiles);
+        const int r = b - mg * G * p.n_tiles;
+        nt = r / G;
+        mt = mg * G + (r - nt * G);
+    };
     int mtile, tile, split, nsplit, q;
     if (bx < F) {
         const int b = ((F & 7) == 0) ? (bx & 7) * (F >> 3) + (bx >> 3) : bx;
-        mtile = b % p.m_tiles_;
-        tile = b / p.m_tiles_;
+        tile_of(b, mtile, tile);
         split = 0;
         nsplit = 1;
         q = 0;
@@ -1740,19 +1758,22 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
         int b = bx;
         const int nwg = gridDim.x;
         if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
-        mtile = b % p.m_tiles_;
-        const int rest = b / p.m_tiles_;
-        split = rest % p.splits;
-        tile = rest / p.splits;
+        if (p.splits == 1) {
+            tile_of(b, mtile, tile);
+            split = 0;
+        } else {
+            mtile = b % p.m_tiles_;
+            const int rest = b / p.m_tiles_;
+            split = rest % p.splits;
+            tile = rest / p.splits;
+        }
         nsplit = p.splits;
         q = tile * p.m_tiles_ + mtile;
     } else {
         const int b = bx - F;
         q = b / p.splits;
         split = b % p.splits;
-        const int tl = F + q;
-        mtile = tl % p.m_tiles_;
-        tile = tl / p.m_tiles_;
+        tile_of(F + q, mtile, tile);
         nsplit = p.splits;
     }
 
