@@ -154,6 +154,25 @@ def test_workspace_sizes_without_gpu(lib):
     assert lib.llmik_w4a16_workspace_size(1, 4096, 4096, 16) > 0
 
 
+@pytest.mark.parametrize("M,N,K,gs,rest,splits", [
+    (768, 14336, 1024, 128, 80, 3),    # 336 tiles: 256 unsplit, 80 in 3 K splits
+    (2048, 14336, 4096, 128, 128, 2),  # 896 tiles: 768 unsplit, 128 in 2
+    (3072, 14336, 1024, 32, 64, 4),    # 1344 tiles: 1280 unsplit, 64 in 4 (group 32)
+    (768, 4096, 14336, 128, 96, 2),    # 96 tiles, each in 2 splits
+    (1024, 14336, 4096, 128, 0, 1),    # 448 tiles: splitting the 192 left costs more
+    (2048, 4096, 4096, 128, 0, 1),     # 256 tiles, one round
+])
+def test_lds_gemm_plans_without_gpu(lib, M, N, K, gs, rest, splits):
+    """The 256 x 128-tile W4A16 GEMM's plan on 256 CUs (the CU count the
+    library assumes without a device): tiles in whole rounds of the CUs run
+    unsplit, the rest split K when the round-cost model says so; the
+    workspace holds the counters and one 256 x 128 fp32 partial per split
+    tile and split."""
+    ws = lib.llmik_w4a16_workspace_size(M, N, K, gs)
+    part = rest * splits * 256 * 128 * 4
+    assert ws == (16384 + (part + 255) // 256 * 256 if splits > 1 else 0)
+
+
 def test_op_surface_matches_reference(mod):
     expect = {
         "decode_attention": ["q", "k", "v", "softmax_scale", "seqlen"],
