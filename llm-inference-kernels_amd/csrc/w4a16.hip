@@ -1980,14 +1980,17 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
                 for (int r = 0; r < 16; ++r) store_res(rb, cb, r, acc[rb][cb][r]);
         return;
     }
-    // Split partials: tile-local [256][128] fp32 slots.
+    // Split partials in the threads' own fragment layout: four-value group j
+    // (acc[rb][cb][4 jj .. 4 jj + 3], j = 4 (2 rb + cb) + jj) of thread t
+    // sits at float offset 4 (512 j + t) of the tile's slot, so every access
+    // instruction moves 16 bytes per lane, contiguous across the lanes, and
+    // the last arriver's thread t reads back exactly the values it adds.
     constexpr uint32_t kTileElems = kL7TM * kL7TN;
-    uint32_t loff[2];   // tile-local element offset of value r = 0 of block row rb
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) loff[rb] = (uint32_t)(64 * wm + 32 * rb + 4 * h) * kL7TN + 64 * wn + c;
-    auto lroff = [&](int r) { return (uint32_t)(8 * (r >> 2) + (r & 3)) * kL7TN; };
     auto part_rsrc = [&](int sp) {
         return make_buffer_rsrc(p.part + ((long)q * nsplit + sp) * kTileElems, kTileElems * 4u);
+    };
+    auto grp_off = [&](int rb, int cb, int jj) {
+        return (uint32_t)((4 * (2 * rb + cb) + jj) * kL7Threads + t) * 16u;
     };
     {
         const __amdgpu_buffer_rsrc_t rp = part_rsrc(split);
@@ -1996,9 +1999,10 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[rb][cb][r]), rp,
-                                                          (int)((loff[rb] + lroff(r) + 32 * cb) * 4u), 0, kPublishAux);
+                for (int jj = 0; jj < 4; ++jj)
+                    publish_store16(rp, grp_off(rb, cb, jj),
+                                    u32x4{__float_as_uint(acc[rb][cb][4 * jj]), __float_as_uint(acc[rb][cb][4 * jj + 1]),
+                                          __float_as_uint(acc[rb][cb][4 * jj + 2]), __float_as_uint(acc[rb][cb][4 * jj + 3])});
     }
     publish_wait();
     __syncthreads();
@@ -2006,33 +2010,43 @@ __global__ __launch_bounds__(kL7Threads) void w4a16_gemm_lds_kernel(GemmParams p
     __syncthreads();
     if (s_last == 0u) return;
     // Last split of the tile: the partials are added in split order (this
-    // workgroup's own from registers, the same bits it stored), one block row
-    // at a time, all loads of one split issued together.
+    // workgroup's own from registers, the same bits it stored), each split's
+    // 64 values per thread loaded together.
+    f32x16 tot[2][2];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        f32x16 tot[2] = {zero16, zero16};
-        for (int sp = 0; sp < nsplit; ++sp) {
-            if (sp == split) {
-                tot[0] += acc[rb][0];
-                tot[1] += acc[rb][1];
-                continue;
-            }
-            const __amdgpu_buffer_rsrc_t rp = part_rsrc(sp);
-            f32x16 x[2];
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) tot[rb][cb] = zero16;
+    for (int sp = 0; sp < nsplit; ++sp) {
+        if (sp == split) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) tot[rb][cb] += acc[rb][cb];
+            continue;
+        }
+        const __amdgpu_buffer_rsrc_t rp = part_rsrc(sp);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    x[cb][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                        rp, (int)((loff[rb] + lroff(r) + 32 * cb) * 4u), 0, kPublishAux));
-            tot[0] += x[0];
-            tot[1] += x[1];
-        }
+                for (int jj = 0; jj < 4; ++jj) {
+                    const u32x4 v = publish_load16(rp, grp_off(rb, cb, jj));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) cg[rb][cb][4 * jj + e] = __uint_as_float(v[e]);
+                }
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) tot[rb][cb] += cg[rb][cb];
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) store_res(rb, cb, r, tot[cb][r]);
-    }
+            for (int r = 0; r < 16; ++r) store_res(rb, cb, r, tot[rb][cb][r]);
     if (t == 0) p.counters[q] = 0u;
 }
 
