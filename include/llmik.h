@@ -235,8 +235,9 @@ LLMIK_API llmik_status llmik_kivi_append_token_int4(
  *   scale         [K/group_size, N] fp16
  * group_size must be a positive multiple of 8 dividing K. act and
  * weight_packed need 16-byte, scale 8-byte and out 4-byte alignment; a
- * 16-byte aligned out lets the M > 16 matrix-core GEMM store 8 / 16 bytes
- * at a time (otherwise it stores one value at a time).
+ * 16-byte aligned out lets the 64 x 128-tile M > 16 matrix-core GEMM store
+ * 8 / 16 bytes at a time (otherwise it stores one value at a time, as the
+ * 256 x 128-tile GEMM that serves M >= 256 with many tiles always does).
  */
 LLMIK_API size_t llmik_w4a16_workspace_size(int M, int N, int K, int group_size);
 
