@@ -88,10 +88,12 @@ def test_llama_shapes(llmik, cuda, M, K, N):
                                       # on 256 CUs): 2 splits with group 32, one split with group
                                       # 64, 2 splits of whole 256-groups, ragged M with 2 splits
                                       # of 6 and 4 stages, a 256-group cut by the split boundary,
-                                      # one and two 64-K stages (the second prologue stage clamped)
+                                      # one and two 64-K stages (the second prologue stage clamped),
+                                      # groups of 512 and 1024 (8 and 16 stages) in 2 splits
                                       (257, 256, 5504, 32), (600, 512, 6144, 64), (300, 1024, 6400, 256),
                                       (1000, 640, 2816, 128), (260, 256, 5632, 256),
-                                      (300, 64, 11008, 32), (513, 128, 11008, 64)])
+                                      (300, 64, 11008, 32), (513, 128, 11008, 64),
+                                      (300, 2048, 6400, 512), (257, 2048, 5504, 1024)])
 def test_odd_shapes(llmik, cuda, M, K, N, gs):
     _check(llmik, cuda, M, K, N, gs, seed=M * 7 + K)
 
