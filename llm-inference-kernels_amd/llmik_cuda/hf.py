@@ -270,9 +270,10 @@ _TARGET_LINEAR_NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "up_proj", "gate
 def dequant_path_threshold(N: int) -> int:
     """Rows from which dequantise + matmul (hipBLASLt) beats w4a16_gemm on
     MI355X, measured at the Llama-3-8B shapes: w4a16_gemm is faster up to
-    1024 rows for N = 4096 (K = 4096 or 14336; 47.6 against 51.7 us and
-    130.6 against 151.0 at 1024, 71.3 against 63.1 at 1536) and up to 768
-    for N = 14336 (106.9 against 112.5). The reference switches at 256
+    1024 rows for N = 4096 (K = 4096 or 14336; 47.1 against 52.6 us and
+    129.1 against 151.5 at 1024, 70.2 against 64.1 at 1536) and up to 768
+    for N = 14336 (113.2 against 114.3; 139.3 against 122.6 at 1024). The
+    reference switches at 256
     (integration/w4a16_patch.py:89), where w4a16_gemm is 2.0-2.4x faster.
     Below the threshold the output is also the exact one (fp32 accumulation
     of unrounded weights, within 2e-3 of the float64 product; the fp16
